@@ -1,0 +1,128 @@
+/*
+ * ns_ffn.h -- C ABI of the MI355X-native quantised FFN path (libnsffn.so).
+ *
+ * Drop-in for the FFN matmul call surface of the reference engine
+ * (src/native/metal_engine.mm, "mm" below): the Q4_K/Q6_K dequant-fused GEMV
+ * and GEMM behind the Gemma-4 gate/up projections, GeGLU, the down projection
+ * and the Q6_K lm-head.  Plain pointers and sizes only.
+ *
+ * Conventions
+ *   - `cols` = K = GGUF shape[0], `rows` = N = GGUF shape[1] (mm:268).
+ *   - Inputs are row-major [batch][cols], outputs [batch][rows] (mm:41-42 args).
+ *   - Weight pointers point at the first byte of the tensor in device memory
+ *     (the reference binds the whole .nsmffn file plus a byte offset, mm:267;
+ *     here the caller adds the offset).  Q4_K tensors must be 16-byte aligned,
+ *     Q6_K tensors 4-byte aligned.
+ *   - Every device entry point is stream-ordered on `stream` (a hipStream_t,
+ *     NULL = the null stream) and never synchronises.
+ *   - Every function returns NS_OK (0) or an error code; ns_last_error() gives
+ *     the message of the last failure on the calling thread.  The C++ wrapper
+ *     (neutron-star_amd/host/ffn_path.hpp) rethrows it as std::runtime_error,
+ *     which is how the reference reports failures (mm:231-243).
+ *   - A context owns the workspace used for split reductions.  Calls that share
+ *     one context must be ordered (one stream, or synchronised); the reference
+ *     serialises all GPU work the same way (mm:137).
+ */
+#ifndef NS_FFN_H
+#define NS_FFN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NS_FFN_ABI_VERSION 1
+
+/* Tensor types: the GGUF ids of include/neutron/native/gguf.hpp:13. */
+enum { NS_TYPE_Q4_K = 12, NS_TYPE_Q6_K = 14 };
+
+/* Byte layouts of a quantised [rows][cols] tensor.
+ *   ROW_MAJOR  GGUF order (src/native/quant.cpp:20, block = element/256).
+ *   NSMFFN     the reference's 64-row slab order (src/native/metal_ffn.cpp:135-149).
+ *   CDNA4      NSMFFN re-tiled into 16-byte chunks per row, lossless (ns_retile). */
+enum { NS_LAYOUT_ROW_MAJOR = 0, NS_LAYOUT_NSMFFN = 1, NS_LAYOUT_CDNA4 = 2 };
+
+/* Accumulation mode of the prefill GEMMs (mm:565 `fast_swa_ffn`).
+ *   FP32  fp32 accumulation (the 8 global layers, and every layer with --exact-ffn).
+ *   FP16  the local-layer mode: the running fp32 sum is rounded to fp16 at every
+ *         256-wide super-block boundary and the result is fp16. */
+enum { NS_ACC_FP32 = 0, NS_ACC_FP16 = 1 };
+
+enum { NS_OK = 0, NS_ERR_ARG = 1, NS_ERR_SHAPE = 2, NS_ERR_HIP = 3, NS_ERR_UNSUPPORTED = 4 };
+
+typedef struct ns_ctx ns_ctx;
+
+const char *ns_last_error(void);
+int ns_abi_version(void);
+
+/* Context on HIP device `device`: owns the split-reduction workspace
+ * (the engine's workspaces, mm:100-101).  No counterpart function in the
+ * reference (the engine constructor does this, mm:90-133). */
+int ns_ctx_create(int device, ns_ctx **out);
+int ns_ctx_destroy(ns_ctx *ctx);
+
+/* NativeMetalEngine::matmul (mm:269-275): out = in . W^T for `batch` tokens.
+ *   batch == 1, fp32 input      -> dequant-fused GEMV (decode; lm-head with ROW_MAJOR or CDNA4).
+ *   batch  > 1, half_input != 0 -> dequant-into-LDS MFMA GEMM, FP32 accumulation.
+ *   batch  > 1, fp32 input      -> one GEMV per token.
+ * `in` is fp32 [batch][cols] or, with half_input, fp16 bits [batch][cols]; out fp32 [batch][rows]. */
+int ns_matmul(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, uint32_t rows,
+              uint32_t batch, const void *in, int half_input, float *out, void *stream);
+
+/* gate_up_geglu_decode (mm:290): h[r] = gelu_tanh(Wg[r].x) * (Wu[r].x), fp32, Q4_K gate/up. */
+int ns_gate_up_geglu_decode(ns_ctx *ctx, const void *wg, const void *wu, int layout,
+                            uint32_t cols, uint32_t rows, const float *x, float *h,
+                            void *stream);
+
+/* gate_up_geglu_rm32 (mm:288): prefill H = gelu_tanh(X.Wg^T) * (X.Wu^T).
+ * x fp16 bits [batch][cols], h fp16 bits [batch][rows]; fast_swa != 0 selects
+ * NS_ACC_FP16 (metal:379), 0 selects NS_ACC_FP32 (metal:373). */
+int ns_gate_up_geglu_rm32(ns_ctx *ctx, const void *wg, const void *wu, int layout,
+                          uint32_t cols, uint32_t rows, uint32_t batch, const uint16_t *x,
+                          uint16_t *h, int fast_swa, void *stream);
+
+/* ffn_down (mm:289): with half_input and batch > 1 the prefill GEMM in the mode
+ * fast_swa selects (metal:480/486 Q6_K, :385/:391 Q4_K); otherwise ns_matmul. */
+int ns_ffn_down(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, uint32_t rows,
+                uint32_t batch, const void *in, int half_input, int fast_swa, float *out,
+                void *stream);
+
+/* Bit-exact check hook: dequantise rows [row0, row0+nrows) to fp32 (quant.cpp:20
+ * values) and/or fp16 (RNE of that fp32, the value the GEMM tiles hold).
+ * Either output may be NULL.  Outputs are [nrows][cols]. */
+int ns_dequant(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, uint32_t rows,
+               uint32_t row0, uint32_t nrows, float *out_f32, uint16_t *out_f16, void *stream);
+
+/* ---- host-side (CPU) utilities; no GPU needed ------------------------------ */
+
+/* Convert a host tensor between layouts (a14; the conversion step of
+ * tools/convert_metal_ffn.cpp).  src and dst must not overlap.  NSMFFN and
+ * CDNA4 need rows % 64 == 0. */
+int ns_retile(const void *src, void *dst, int type, uint32_t cols, uint32_t rows,
+              int from_layout, int to_layout);
+
+/* Same conversion on device memory, stream-ordered. */
+int ns_retile_device(const void *src, void *dst, int type, uint32_t cols, uint32_t rows,
+                     int from_layout, int to_layout, void *stream);
+
+/* Seeded synthetic data (this build's generator; configs of BASELINE.json).
+ * Blocks [first, first+count) of a tensor with seed `seed`, ROW_MAJOR block
+ * order, written contiguously to out (count * 144 or 210 bytes).
+ *   Q4_K: d, dmin = fp16(|N(0,1)| * 1e-3); scales[12], qs[128] uniform bytes.
+ *   Q6_K: ql[128], qh[64] uniform bytes; scales int8 uniform in -32..31;
+ *         d = fp16(|N(0,1)| * 1e-3). */
+int ns_synth_blocks(int type, uint64_t seed, uint64_t first, uint64_t count, void *out,
+                    int nthreads);
+/* N(0,1) values [first, first+count) of stream `seed`, fp32 or fp16 (RNE of the fp32). */
+int ns_synth_normal_f32(uint64_t seed, uint64_t first, uint64_t count, float *out, int nthreads);
+int ns_synth_normal_f16(uint64_t seed, uint64_t first, uint64_t count, uint16_t *out,
+                        int nthreads);
+/* Per-layer seed: seed ^ (layer * 0x9E3779B97F4A7C15). */
+uint64_t ns_layer_seed(uint64_t seed, uint32_t layer);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NS_FFN_H */

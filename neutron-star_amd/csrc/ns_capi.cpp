@@ -1,0 +1,192 @@
+// ns_capi.cpp -- the extern "C" boundary (include/ns_ffn.h): argument
+// validation, the context/workspace, and regime dispatch mirroring the
+// reference engine's helpers (src/native/metal_engine.mm:269-290).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <mutex>
+#include <string>
+
+#include "ns_ffn.h"
+#include "ns_internal.hpp"
+
+struct ns_ctx {
+    int device = 0;
+    ns::Workspace ws;
+};
+
+namespace {
+using namespace ns;
+
+int fail(int code, const std::string &msg) {
+    set_error(msg);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(NS_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// The reference accepts cols % 256 == 0 and rows % 64 == 0 (metal_ffn.cpp:74).
+int check_tensor(const char *fn, const void *w, int type, int layout, uint32_t cols, uint32_t rows) {
+    if (!w) return fail(NS_ERR_ARG, std::string(fn) + ": null weight pointer");
+    if (type != Q4_K && type != Q6_K) return fail(NS_ERR_ARG, std::string(fn) + ": type must be Q4_K or Q6_K");
+    if (layout != ROW_MAJOR && layout != NSMFFN && layout != CDNA4)
+        return fail(NS_ERR_ARG, std::string(fn) + ": unknown layout");
+    if (cols == 0 || cols % kQK) return fail(NS_ERR_SHAPE, std::string(fn) + ": cols must be a positive multiple of 256");
+    if (rows == 0 || (layout != ROW_MAJOR && rows % kRowTile))
+        return fail(NS_ERR_SHAPE, std::string(fn) + ": rows must be a positive multiple of 64 for slab layouts");
+    const uintptr_t a = reinterpret_cast<uintptr_t>(w);
+    if ((type == Q4_K && a % 16) || (type == Q6_K && a % 4))
+        return fail(NS_ERR_ARG, std::string(fn) + ": weight pointer misaligned");
+    return NS_OK;
+}
+
+// Grows the context workspace; the old buffers may still be read by queued
+// work, so the device is drained first (growth happens once per new shape).
+int ensure_ws(ns_ctx *ctx, size_t partial_floats, size_t counters) {
+    if (partial_floats <= ctx->ws.partial_floats && counters <= ctx->ws.counter_count) return NS_OK;
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) return hip_fail(e, "workspace growth");
+    if (partial_floats > ctx->ws.partial_floats) {
+        if (ctx->ws.partial) (void)hipFree(ctx->ws.partial);
+        ctx->ws.partial = nullptr;
+        ctx->ws.partial_floats = 0;
+        e = hipMalloc(reinterpret_cast<void **>(&ctx->ws.partial), partial_floats * sizeof(float));
+        if (e != hipSuccess) return hip_fail(e, "workspace allocation");
+        ctx->ws.partial_floats = partial_floats;
+    }
+    if (counters > ctx->ws.counter_count) {
+        if (ctx->ws.counters) (void)hipFree(ctx->ws.counters);
+        ctx->ws.counters = nullptr;
+        ctx->ws.counter_count = 0;
+        e = hipMalloc(reinterpret_cast<void **>(&ctx->ws.counters), counters * sizeof(uint32_t));
+        if (e == hipSuccess) e = hipMemset(ctx->ws.counters, 0, counters * sizeof(uint32_t));
+        if (e != hipSuccess) return hip_fail(e, "workspace allocation");
+        ctx->ws.counter_count = counters;
+    }
+    return NS_OK;
+}
+
+int gemv(ns_ctx *ctx, const char *fn, int type, int layout, const void *w, const void *up, const float *x,
+         float *out, uint32_t cols, uint32_t rows, hipStream_t s) {
+    size_t pf = 0, nc = 0;
+    gemv_workspace_need(cols, rows, up != nullptr, &pf, &nc);
+    if (int rc = ensure_ws(ctx, pf, nc)) return rc;
+    const hipError_t e = launch_gemv(type, layout, static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(up),
+                                     x, out, cols, rows, ctx->ws, s);
+    return e == hipSuccess ? NS_OK : hip_fail(e, fn);
+}
+
+int gemm(ns_ctx *ctx, const char *fn, int type, int layout, int acc, const void *w, const void *up,
+         const uint16_t *x, void *out, uint32_t cols, uint32_t rows, uint32_t batch, hipStream_t s) {
+    if (layout == ROW_MAJOR)
+        return fail(NS_ERR_UNSUPPORTED, std::string(fn) + ": the prefill GEMM needs the NSMFFN or CDNA4 slab layout");
+    const hipError_t e = launch_gemm(type, layout, acc, static_cast<const uint8_t *>(w),
+                                     static_cast<const uint8_t *>(up), x, out, cols, rows, batch, ctx->ws, s);
+    return e == hipSuccess ? NS_OK : hip_fail(e, fn);
+}
+
+}  // namespace
+
+extern "C" int ns_ctx_create(int device, ns_ctx **out) {
+    if (!out) return fail(NS_ERR_ARG, "ns_ctx_create: null output");
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) return hip_fail(e, "ns_ctx_create");
+    if (device < 0 || device >= n) return fail(NS_ERR_ARG, "ns_ctx_create: no such device");
+    e = hipSetDevice(device);
+    if (e != hipSuccess) return hip_fail(e, "ns_ctx_create");
+    auto *ctx = new ns_ctx;
+    ctx->device = device;
+    // Enough for every shape of the supported model without growth.
+    if (int rc = ensure_ws(ctx, size_t(8) << 20, size_t(1) << 16)) {
+        ns_ctx_destroy(ctx);
+        return rc;
+    }
+    *out = ctx;
+    return NS_OK;
+}
+
+extern "C" int ns_ctx_destroy(ns_ctx *ctx) {
+    if (!ctx) return NS_OK;
+    (void)hipSetDevice(ctx->device);
+    (void)hipDeviceSynchronize();
+    if (ctx->ws.partial) (void)hipFree(ctx->ws.partial);
+    if (ctx->ws.counters) (void)hipFree(ctx->ws.counters);
+    delete ctx;
+    return NS_OK;
+}
+
+extern "C" int ns_matmul(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, uint32_t rows,
+                         uint32_t batch, const void *in, int half_input, float *out, void *stream) {
+    if (!ctx) return fail(NS_ERR_ARG, "ns_matmul: null context");
+    if (int rc = check_tensor("ns_matmul", w, type, layout, cols, rows)) return rc;
+    if (!in || !out || batch == 0) return fail(NS_ERR_ARG, "ns_matmul: null input/output or zero batch");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (half_input && batch > 1)
+        return gemm(ctx, "ns_matmul", type, layout, ACC_FP32, w, nullptr, static_cast<const uint16_t *>(in), out,
+                    cols, rows, batch, s);
+    if (half_input) return fail(NS_ERR_UNSUPPORTED, "ns_matmul: fp16 input at batch 1 is not a reference regime");
+    const auto *x = static_cast<const float *>(in);
+    for (uint32_t t = 0; t < batch; ++t)
+        if (int rc = gemv(ctx, "ns_matmul", type, layout, w, nullptr, x + size_t(t) * cols, out + size_t(t) * rows,
+                          cols, rows, s))
+            return rc;
+    return NS_OK;
+}
+
+extern "C" int ns_gate_up_geglu_decode(ns_ctx *ctx, const void *wg, const void *wu, int layout, uint32_t cols,
+                                       uint32_t rows, const float *x, float *h, void *stream) {
+    if (!ctx) return fail(NS_ERR_ARG, "ns_gate_up_geglu_decode: null context");
+    if (int rc = check_tensor("ns_gate_up_geglu_decode", wg, Q4_K, layout, cols, rows)) return rc;
+    if (int rc = check_tensor("ns_gate_up_geglu_decode", wu, Q4_K, layout, cols, rows)) return rc;
+    if (!x || !h) return fail(NS_ERR_ARG, "ns_gate_up_geglu_decode: null input/output");
+    return gemv(ctx, "ns_gate_up_geglu_decode", Q4_K, layout, wg, wu, x, h, cols, rows,
+                static_cast<hipStream_t>(stream));
+}
+
+extern "C" int ns_gate_up_geglu_rm32(ns_ctx *ctx, const void *wg, const void *wu, int layout, uint32_t cols,
+                                     uint32_t rows, uint32_t batch, const uint16_t *x, uint16_t *h, int fast_swa,
+                                     void *stream) {
+    if (!ctx) return fail(NS_ERR_ARG, "ns_gate_up_geglu_rm32: null context");
+    if (int rc = check_tensor("ns_gate_up_geglu_rm32", wg, Q4_K, layout, cols, rows)) return rc;
+    if (int rc = check_tensor("ns_gate_up_geglu_rm32", wu, Q4_K, layout, cols, rows)) return rc;
+    if (!x || !h || batch == 0) return fail(NS_ERR_ARG, "ns_gate_up_geglu_rm32: null input/output or zero batch");
+    return gemm(ctx, "ns_gate_up_geglu_rm32", Q4_K, layout, fast_swa ? ACC_FP16 : ACC_FP32, wg, wu, x, h, cols,
+                rows, batch, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int ns_ffn_down(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, uint32_t rows,
+                           uint32_t batch, const void *in, int half_input, int fast_swa, float *out, void *stream) {
+    if (!ctx) return fail(NS_ERR_ARG, "ns_ffn_down: null context");
+    if (half_input && batch > 1) {
+        if (int rc = check_tensor("ns_ffn_down", w, type, layout, cols, rows)) return rc;
+        if (!in || !out) return fail(NS_ERR_ARG, "ns_ffn_down: null input/output");
+        return gemm(ctx, "ns_ffn_down", type, layout, fast_swa ? ACC_FP16 : ACC_FP32, w, nullptr,
+                    static_cast<const uint16_t *>(in), out, cols, rows, batch, static_cast<hipStream_t>(stream));
+    }
+    return ns_matmul(ctx, w, type, layout, cols, rows, batch, in, half_input, out, stream);
+}
+
+extern "C" int ns_dequant(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, uint32_t rows,
+                          uint32_t row0, uint32_t nrows, float *out_f32, uint16_t *out_f16, void *stream) {
+    if (!ctx) return fail(NS_ERR_ARG, "ns_dequant: null context");
+    if (int rc = check_tensor("ns_dequant", w, type, layout, cols, rows)) return rc;
+    if (uint64_t(row0) + nrows > rows) return fail(NS_ERR_SHAPE, "ns_dequant: row range out of bounds");
+    const hipError_t e = launch_dequant(type, layout, static_cast<const uint8_t *>(w), cols, rows, row0, nrows,
+                                        out_f32, out_f16, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? NS_OK : hip_fail(e, "ns_dequant");
+}
+
+extern "C" int ns_retile_device(const void *src, void *dst, int type, uint32_t cols, uint32_t rows, int from_layout,
+                                int to_layout, void *stream) {
+    if (int rc = check_tensor("ns_retile_device", src, type, from_layout, cols, rows)) return rc;
+    if (int rc = check_tensor("ns_retile_device", dst, type, to_layout, cols, rows)) return rc;
+    if (src == dst) return fail(NS_ERR_ARG, "ns_retile_device: in-place conversion is not supported");
+    const hipError_t e = launch_retile(type, static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), cols,
+                                       rows, from_layout, to_layout, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? NS_OK : hip_fail(e, "ns_retile_device");
+}

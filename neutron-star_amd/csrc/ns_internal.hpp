@@ -1,0 +1,48 @@
+// ns_internal.hpp -- launchers and helpers shared by the C-ABI layer and the kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "ns_common.hpp"
+
+namespace ns {
+
+// Thread-local error text behind ns_last_error().
+void set_error(const std::string &msg);
+
+// Workspace owned by ns_ctx: fp32 partial sums and per-slab arrival counters
+// for reductions that span workgroups.  Counters are zero between calls (the
+// last workgroup of a slab resets its counter).
+struct Workspace {
+    float *partial = nullptr;
+    size_t partial_floats = 0;
+    uint32_t *counters = nullptr;
+    size_t counter_count = 0;
+};
+
+// Decode GEMV: out[r] = sum_k W[r,k] x[k] (fp32).  With `up` non-null, the
+// gate/up pair with the GeGLU epilogue (out = h).  Returns a hipError_t.
+hipError_t launch_gemv(int type, int layout, const uint8_t *w, const uint8_t *up,
+                       const float *x, float *out, uint32_t cols, uint32_t rows,
+                       const Workspace &ws, hipStream_t stream);
+
+// Required workspace for launch_gemv with these shapes.
+void gemv_workspace_need(uint32_t cols, uint32_t rows, bool pair, size_t *partial_floats,
+                         size_t *counters);
+
+// Prefill GEMM over fp16 x [batch][cols]: plain (fp32 out [batch][rows]) or the
+// gate/up pair with GeGLU (fp16 h [batch][rows]).
+hipError_t launch_gemm(int type, int layout, int acc, const uint8_t *w, const uint8_t *up,
+                       const uint16_t *x, void *out, uint32_t cols, uint32_t rows,
+                       uint32_t batch, const Workspace &ws, hipStream_t stream);
+
+hipError_t launch_dequant(int type, int layout, const uint8_t *w, uint32_t cols, uint32_t rows,
+                          uint32_t row0, uint32_t nrows, float *out_f32, uint16_t *out_f16,
+                          hipStream_t stream);
+
+hipError_t launch_retile(int type, const uint8_t *src, uint8_t *dst, uint32_t cols,
+                         uint32_t rows, int from_layout, int to_layout, hipStream_t stream);
+
+}  // namespace ns

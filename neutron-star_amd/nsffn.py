@@ -1,0 +1,177 @@
+"""ctypes binding of libnsffn.so (include/ns_ffn.h) for tests, smoke and bench.
+
+Device buffers are torch tensors (PyTorch is only used for device memory and
+streams); host utilities take numpy arrays.  Loading fails loudly when the
+library has not been built: there is no fallback path.
+"""
+import ctypes
+import os
+import re
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+LIB_PATH = os.path.join(PKG, "libnsffn.so")
+HEADER = os.path.join(ROOT, "include", "ns_ffn.h")
+
+Q4_K, Q6_K = 12, 14
+ROW_MAJOR, NSMFFN, CDNA4 = 0, 1, 2
+ACC_FP32, ACC_FP16 = 0, 1
+BLOCK_BYTES = {Q4_K: 144, Q6_K: 210}
+
+_lib = None
+
+
+class NsError(RuntimeError):
+    """A non-zero status from the C ABI, with ns_last_error()'s message."""
+
+    def __init__(self, code, msg):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+def header_functions():
+    """Names of the functions declared in include/ns_ffn.h."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ns_[a-z0-9_]+)\s*\(", text)))
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built: run __graft_entry__.build()")
+        L = ctypes.CDLL(LIB_PATH)
+        vp, u32, u64, i32 = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int
+        L.ns_last_error.restype = ctypes.c_char_p
+        L.ns_layer_seed.restype = u64
+        L.ns_layer_seed.argtypes = [u64, u32]
+        sigs = {
+            "ns_abi_version": [],
+            "ns_ctx_create": [i32, ctypes.POINTER(vp)],
+            "ns_ctx_destroy": [vp],
+            "ns_matmul": [vp, vp, i32, i32, u32, u32, u32, vp, i32, vp, vp],
+            "ns_gate_up_geglu_decode": [vp, vp, vp, i32, u32, u32, vp, vp, vp],
+            "ns_gate_up_geglu_rm32": [vp, vp, vp, i32, u32, u32, u32, vp, vp, i32, vp],
+            "ns_ffn_down": [vp, vp, i32, i32, u32, u32, u32, vp, i32, i32, vp, vp],
+            "ns_dequant": [vp, vp, i32, i32, u32, u32, u32, u32, vp, vp, vp],
+            "ns_retile": [vp, vp, i32, u32, u32, i32, i32],
+            "ns_retile_device": [vp, vp, i32, u32, u32, i32, i32, vp],
+            "ns_synth_blocks": [i32, u64, u64, u64, vp, i32],
+            "ns_synth_normal_f32": [u64, u64, u64, vp, i32],
+            "ns_synth_normal_f16": [u64, u64, u64, vp, i32],
+        }
+        for name, args in sigs.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc != 0:
+        raise NsError(rc, lib().ns_last_error().decode())
+    return rc
+
+
+def _ptr(a):
+    if a is None:
+        return None
+    if isinstance(a, np.ndarray):
+        return a.ctypes.data
+    return a.data_ptr()
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    return stream
+
+
+def default_threads():
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+# ---- host utilities --------------------------------------------------------
+
+def synth_blocks(qtype, seed, nblocks, first=0, nthreads=None):
+    out = np.empty(nblocks * BLOCK_BYTES[qtype], dtype=np.uint8)
+    check(lib().ns_synth_blocks(qtype, seed, first, nblocks, _ptr(out), nthreads or default_threads()))
+    return out
+
+
+def synth_weights(qtype, seed, rows, cols, nthreads=None):
+    """ROW_MAJOR bytes of a seeded [rows][cols] tensor (block i = row*nb + kb)."""
+    return synth_blocks(qtype, seed, rows * (cols // 256), nthreads=nthreads)
+
+
+def synth_normal_f32(seed, n, first=0, nthreads=None):
+    out = np.empty(n, dtype=np.float32)
+    check(lib().ns_synth_normal_f32(seed, first, n, _ptr(out), nthreads or default_threads()))
+    return out
+
+
+def synth_normal_f16(seed, n, first=0, nthreads=None):
+    out = np.empty(n, dtype=np.uint16)
+    check(lib().ns_synth_normal_f16(seed, first, n, _ptr(out), nthreads or default_threads()))
+    return out
+
+
+def layer_seed(seed, layer):
+    return lib().ns_layer_seed(seed, layer)
+
+
+def retile(src, qtype, cols, rows, from_layout, to_layout):
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    dst = np.empty_like(src)
+    check(lib().ns_retile(_ptr(src), _ptr(dst), qtype, cols, rows, from_layout, to_layout))
+    return dst
+
+
+# ---- device entry points (torch tensors) ------------------------------------
+
+class Context:
+    def __init__(self, device=0):
+        h = ctypes.c_void_p()
+        check(lib().ns_ctx_create(device, ctypes.byref(h)))
+        self.handle = h
+
+    def close(self):
+        if self.handle:
+            lib().ns_ctx_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def matmul(self, w, qtype, layout, cols, rows, batch, inp, out, half_input=False, stream=None):
+        check(lib().ns_matmul(self.handle, _ptr(w), qtype, layout, cols, rows, batch, _ptr(inp),
+                              int(half_input), _ptr(out), _stream(stream)))
+
+    def gate_up_geglu_decode(self, wg, wu, layout, cols, rows, x, h, stream=None):
+        check(lib().ns_gate_up_geglu_decode(self.handle, _ptr(wg), _ptr(wu), layout, cols, rows,
+                                            _ptr(x), _ptr(h), _stream(stream)))
+
+    def gate_up_geglu_rm32(self, wg, wu, layout, cols, rows, batch, x, h, fast_swa, stream=None):
+        check(lib().ns_gate_up_geglu_rm32(self.handle, _ptr(wg), _ptr(wu), layout, cols, rows, batch,
+                                          _ptr(x), _ptr(h), int(fast_swa), _stream(stream)))
+
+    def ffn_down(self, w, qtype, layout, cols, rows, batch, inp, out, half_input, fast_swa, stream=None):
+        check(lib().ns_ffn_down(self.handle, _ptr(w), qtype, layout, cols, rows, batch, _ptr(inp),
+                                int(half_input), int(fast_swa), _ptr(out), _stream(stream)))
+
+    def dequant(self, w, qtype, layout, cols, rows, row0, nrows, out_f32=None, out_f16=None, stream=None):
+        check(lib().ns_dequant(self.handle, _ptr(w), qtype, layout, cols, rows, row0, nrows,
+                               _ptr(out_f32), _ptr(out_f16), _stream(stream)))
+
+
+def retile_device(src, dst, qtype, cols, rows, from_layout, to_layout, stream=None):
+    check(lib().ns_retile_device(_ptr(src), _ptr(dst), qtype, cols, rows, from_layout, to_layout,
+                                 _stream(stream)))

@@ -1,0 +1,270 @@
+/*
+ * ns_oracle.c -- CPU restatement of the reference's quantized FFN arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker and the timed CPU baseline); see
+ * ns_oracle.h for the list of reference lines each function follows and for
+ * what pins each one.  Built with -ffp-contract=off so that every fp32 sum is
+ * the sequential, uncontracted sum that quant.cpp:21 writes.
+ */
+#include "ns_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- fp16 <-> fp32 (IEEE binary16, round to nearest even) ---------------- */
+
+float nso_f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t exp = (h >> 10) & 0x1fu;
+    const uint32_t mant = h & 0x3ffu;
+    uint32_t bits;
+    if (exp == 0) {
+        /* zero or subnormal: mant * 2^-24, exact in fp32 */
+        float v = (float)mant * 5.9604644775390625e-08f;
+        return sign ? -v : v;
+    } else if (exp == 31) {
+        bits = sign | 0x7f800000u | (mant << 13);
+    } else {
+        bits = sign | ((exp - 15 + 127) << 23) | (mant << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+uint16_t nso_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    const uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) return sign | (ax > 0x7f800000u ? 0x7e00u : 0x7c00u);
+    if (ax >= 0x477ff000u) return sign | 0x7c00u; /* >= 65520 rounds to inf */
+    if (ax < 0x38800000u) {                       /* below 2^-14: subnormal half */
+        if (ax < 0x33000000u) return sign;        /* <= 2^-25 rounds to zero */
+        const uint32_t e = ax >> 23;
+        const uint32_t mant = (ax & 0x7fffffu) | 0x800000u;
+        const uint32_t shift = 126u - e;           /* 14..24 */
+        uint32_t r = mant >> shift;
+        const uint32_t rem = mant & ((1u << shift) - 1u), half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (r & 1u))) ++r;
+        return sign | (uint16_t)r;
+    }
+    const uint32_t e16 = (ax >> 23) - 127u + 15u;
+    uint32_t r = (e16 << 10) | ((ax >> 13) & 0x3ffu);
+    const uint32_t rem = ax & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) ++r;
+    return sign | (uint16_t)r;
+}
+
+static float round_f16(float v) { return nso_f16_to_f32(nso_f32_to_f16(v)); }
+
+/* ---- element values (quant.cpp:9-18) ------------------------------------ */
+
+static float rd_f16(const uint8_t *p) { return nso_f16_to_f32((uint16_t)(p[0] | (p[1] << 8))); }
+
+/* quant.cpp:9-12: 8 groups of 32; 6-bit scale/min unpack; w = d*sc*q - dmin*m. */
+float nso_q4k_value(const uint8_t *b, uint32_t i) {
+    const float d = rd_f16(b), dm = rd_f16(b + 2);
+    const uint8_t *s = b + 4, *q = b + 16;
+    const uint32_t g = i / 32, l = i % 32;
+    uint8_t sc, m;
+    if (g < 4) {
+        sc = s[g] & 63;
+        m = s[g + 4] & 63;
+    } else {
+        sc = (uint8_t)((s[g + 4] & 15) | ((s[g - 4] >> 6) << 4));
+        m = (uint8_t)((s[g + 4] >> 4) | ((s[g] >> 6) << 4));
+    }
+    const uint8_t v = (g & 1) ? (uint8_t)(q[(g / 2) * 32 + l] >> 4) : (uint8_t)(q[(g / 2) * 32 + l] & 15);
+    return d * sc * v - dm * m;
+}
+
+/* quant.cpp:13-18: 6-bit value from ql nibble + qh 2 bits; w = d*sc*(v-32). */
+float nso_q6k_value(const uint8_t *b, uint32_t i) {
+    const uint8_t *ql = b, *qh = b + 128;
+    const int8_t *sc = (const int8_t *)(b + 192);
+    const float d = rd_f16(b + 208);
+    const uint32_t half = i / 128, p = i % 128, l = p % 32, quarter = p / 32;
+    const uint8_t *lo = ql + half * 64, *hi = qh + half * 32;
+    int v;
+    if (quarter == 0) v = (lo[l] & 15) | (((hi[l] >> 0) & 3) << 4);
+    else if (quarter == 1) v = (lo[l + 32] & 15) | (((hi[l] >> 2) & 3) << 4);
+    else if (quarter == 2) v = (lo[l] >> 4) | (((hi[l] >> 4) & 3) << 4);
+    else v = (lo[l + 32] >> 4) | (((hi[l] >> 6) & 3) << 4);
+    return d * sc[half * 8 + (l / 16) + quarter * 2] * (v - 32);
+}
+
+/* ---- layouts -------------------------------------------------------------- */
+
+/* ROW_MAJOR: GGUF order (quant.cpp:20 block = e/256).  NSMFFN:
+ * metal_ffn.cpp:145-146 target = ((row0/64)*blocks + block)*64 + row. */
+uint64_t nso_block_index(int layout, uint64_t row, uint64_t kblock, uint64_t nb) {
+    if (layout == NSO_NSMFFN) return ((row / 64) * nb + kblock) * 64 + row % 64;
+    return row * nb + kblock;
+}
+
+static size_t block_bytes(int type) { return type == NSO_Q4_K ? 144 : 210; }
+
+static int check(int type, int layout, uint64_t cols, uint64_t rows) {
+    if (type != NSO_Q4_K && type != NSO_Q6_K) return -1;
+    if (layout != NSO_ROW_MAJOR && layout != NSO_NSMFFN) return -1;
+    if (cols % 256) return -1;
+    if (layout == NSO_NSMFFN && rows % 64) return -1;
+    return 0;
+}
+
+int nso_dequant_row(int type, int layout, const uint8_t *w, uint64_t cols, uint64_t rows,
+                    uint64_t row, float *out) {
+    if (check(type, layout, cols, rows) || row >= rows) return -1;
+    const uint64_t nb = cols / 256;
+    const size_t bs = block_bytes(type);
+    for (uint64_t b = 0; b < nb; ++b) {
+        const uint8_t *blk = w + nso_block_index(layout, row, b, nb) * bs;
+        for (uint32_t i = 0; i < 256; ++i)
+            out[b * 256 + i] = type == NSO_Q4_K ? nso_q4k_value(blk, i) : nso_q6k_value(blk, i);
+    }
+    return 0;
+}
+
+/* quant.cpp:21: float sum=0; for i<cols: sum += dequant(row*cols+i) * x[i]. */
+float nso_dot_row(int type, int layout, const uint8_t *w, uint64_t cols, uint64_t rows,
+                  uint64_t row, const float *x) {
+    (void)rows;
+    const uint64_t nb = cols / 256;
+    const size_t bs = block_bytes(type);
+    float sum = 0;
+    for (uint64_t i = 0; i < cols; ++i) {
+        const uint8_t *blk = w + nso_block_index(layout, row, i / 256, nb) * bs;
+        const float v = type == NSO_Q4_K ? nso_q4k_value(blk, (uint32_t)(i % 256))
+                                         : nso_q6k_value(blk, (uint32_t)(i % 256));
+        sum += v * x[i];
+    }
+    return sum;
+}
+
+/* metal/gemma4.metal:78 -- 0.5*g*(1+tanh(0.79788456*g*(1+0.044715*g*g))). */
+float nso_gelu_tanh(float g) {
+    return 0.5f * g * (1.0f + tanhf(0.7978845608028654f * g * (1.0f + 0.044715f * g * g)));
+}
+
+/* ---- threaded drivers ---------------------------------------------------- */
+
+typedef struct {
+    int type, layout, acc_mode;
+    const uint8_t *w;
+    uint64_t cols, rows, batch;
+    const float *x;       /* gemv: fp32 x[cols] */
+    const float *xt;      /* gemm: fp32 copy of x transposed [cols][batch] */
+    float *out;           /* gemv: [rows]; gemm: [batch][rows] */
+    uint64_t r0, r1;
+} job_t;
+
+static void *gemv_worker(void *p) {
+    job_t *j = (job_t *)p;
+    float *row = (float *)malloc(j->cols * sizeof(float));
+    for (uint64_t r = j->r0; r < j->r1; ++r) {
+        nso_dequant_row(j->type, j->layout, j->w, j->cols, j->rows, r, row);
+        float sum = 0;
+        for (uint64_t k = 0; k < j->cols; ++k) sum += row[k] * j->x[k];
+        j->out[r] = sum;
+    }
+    free(row);
+    return NULL;
+}
+
+/* Row dequantised once; the token loop is innermost so each acc[t] is its own
+ * sequential k-order sum (vectorised across tokens only). */
+static void *gemm_worker(void *p) {
+    job_t *j = (job_t *)p;
+    const uint64_t B = j->batch;
+    float *row = (float *)malloc(j->cols * sizeof(float));
+    float *acc = (float *)malloc(B * sizeof(float));
+    for (uint64_t r = j->r0; r < j->r1; ++r) {
+        nso_dequant_row(j->type, j->layout, j->w, j->cols, j->rows, r, row);
+        for (uint64_t t = 0; t < B; ++t) acc[t] = 0;
+        for (uint64_t k = 0; k < j->cols; ++k) {
+            const float wk = row[k];
+            const float *xk = j->xt + k * B;
+            for (uint64_t t = 0; t < B; ++t) acc[t] += wk * xk[t];
+            if (j->acc_mode == 1 && (k % 256) == 255)
+                for (uint64_t t = 0; t < B; ++t) acc[t] = round_f16(acc[t]);
+        }
+        for (uint64_t t = 0; t < B; ++t) j->out[t * j->rows + r] = acc[t];
+    }
+    free(acc);
+    free(row);
+    return NULL;
+}
+
+static int run_rows(job_t *base, uint64_t rows, int nthreads, void *(*fn)(void *)) {
+    if (nthreads < 1) nthreads = 1;
+    if ((uint64_t)nthreads > rows) nthreads = (int)(rows ? rows : 1);
+    pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)nthreads);
+    job_t *jobs = (job_t *)malloc(sizeof(job_t) * (size_t)nthreads);
+    for (int i = 0; i < nthreads; ++i) {
+        jobs[i] = *base;
+        jobs[i].r0 = rows * (uint64_t)i / (uint64_t)nthreads;
+        jobs[i].r1 = rows * (uint64_t)(i + 1) / (uint64_t)nthreads;
+        pthread_create(&th[i], NULL, fn, &jobs[i]);
+    }
+    for (int i = 0; i < nthreads; ++i) pthread_join(th[i], NULL);
+    free(jobs);
+    free(th);
+    return 0;
+}
+
+int nso_gemv(int type, int layout, const uint8_t *w, uint64_t cols, uint64_t rows,
+             const float *x, float *y, int nthreads) {
+    if (check(type, layout, cols, rows)) return -1;
+    job_t j;
+    memset(&j, 0, sizeof j);
+    j.type = type; j.layout = layout; j.w = w; j.cols = cols; j.rows = rows; j.x = x; j.out = y;
+    return run_rows(&j, rows, nthreads, gemv_worker);
+}
+
+int nso_gate_up_geglu(int layout, const uint8_t *wg, const uint8_t *wu, uint64_t cols,
+                      uint64_t rows, const float *x, float *h, int nthreads) {
+    float *g = (float *)malloc(rows * sizeof(float));
+    float *u = (float *)malloc(rows * sizeof(float));
+    int rc = nso_gemv(NSO_Q4_K, layout, wg, cols, rows, x, g, nthreads);
+    if (!rc) rc = nso_gemv(NSO_Q4_K, layout, wu, cols, rows, x, u, nthreads);
+    if (!rc)
+        for (uint64_t r = 0; r < rows; ++r) h[r] = nso_gelu_tanh(g[r]) * u[r];
+    free(g);
+    free(u);
+    return rc;
+}
+
+int nso_gemm(int type, int layout, const uint8_t *w, uint64_t cols, uint64_t rows,
+             uint64_t batch, const uint16_t *x_f16, int acc_mode, float *out, int nthreads) {
+    if (check(type, layout, cols, rows) || (acc_mode != 0 && acc_mode != 1)) return -1;
+    float *xt = (float *)malloc(cols * batch * sizeof(float));
+    if (!xt) return -1;
+    for (uint64_t t = 0; t < batch; ++t)
+        for (uint64_t k = 0; k < cols; ++k) xt[k * batch + t] = nso_f16_to_f32(x_f16[t * cols + k]);
+    job_t j;
+    memset(&j, 0, sizeof j);
+    j.type = type; j.layout = layout; j.acc_mode = acc_mode; j.w = w; j.cols = cols;
+    j.rows = rows; j.batch = batch; j.xt = xt; j.out = out;
+    run_rows(&j, rows, nthreads, gemm_worker);
+    free(xt);
+    if (acc_mode == 1) /* FP16 mode: outputs are fp16 values (metal:394, :489 widen half) */
+        for (uint64_t i = 0; i < rows * batch; ++i) out[i] = round_f16(out[i]);
+    return 0;
+}
+
+int nso_gate_up_geglu_prefill(int layout, const uint8_t *wg, const uint8_t *wu, uint64_t cols,
+                              uint64_t rows, uint64_t batch, const uint16_t *x_f16,
+                              int acc_mode, float *h, int nthreads) {
+    float *g = (float *)malloc(rows * batch * sizeof(float));
+    float *u = (float *)malloc(rows * batch * sizeof(float));
+    int rc = nso_gemm(NSO_Q4_K, layout, wg, cols, rows, batch, x_f16, acc_mode, g, nthreads);
+    if (!rc) rc = nso_gemm(NSO_Q4_K, layout, wu, cols, rows, batch, x_f16, acc_mode, u, nthreads);
+    if (!rc)
+        for (uint64_t i = 0; i < rows * batch; ++i) h[i] = nso_gelu_tanh(g[i]) * u[i];
+    free(g);
+    free(u);
+    return rc;
+}

@@ -1,0 +1,260 @@
+"""GPU parity tests: the HIP path, called through the C ABI, against the CPU
+oracle on identical seeded inputs.
+
+Bars:
+  dequantised weights      bit-exact (fp32 and its fp16 RNE)
+  FP32-accumulation output rel_err <= 1e-3
+  FP16-accumulation output rel_err <= 1e-2
+rel_err (tests/helpers.py) = max over output rows of max|got-ref| / max|ref|.
+"""
+import numpy as np
+import pytest
+
+import ns_oracle as O
+import nsffn as N
+from helpers import f16_value, rel_err
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+TOL32, TOL16 = 1e-3, 1e-2
+LAYOUTS = [N.CDNA4, N.NSMFFN, N.ROW_MAJOR]
+LNAME = {N.CDNA4: "cdna4", N.NSMFFN: "nsmffn", N.ROW_MAJOR: "rowmajor"}
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    assert torch.cuda.is_available(), "GPU tests need a visible MI355X"
+    c = N.Context(0)
+    yield c
+    torch.cuda.synchronize()
+    c.close()
+
+
+def dev_bytes(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def dev_u16(a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda()
+
+
+def weights(qtype, seed, rows, cols, layout):
+    """(oracle ROW_MAJOR bytes, device bytes in `layout`)."""
+    host = N.synth_weights(qtype, seed, rows, cols)
+    lay = host if layout == N.ROW_MAJOR else N.retile(host, qtype, cols, rows, N.ROW_MAJOR, layout)
+    return host, dev_bytes(lay)
+
+
+def f32(n, seed):
+    return N.synth_normal_f32(seed, n)
+
+
+# ---- dequantisation: bit-exact ------------------------------------------------
+
+@pytest.mark.parametrize("layout", LAYOUTS, ids=LNAME.get)
+@pytest.mark.parametrize("qtype", [N.Q4_K, N.Q6_K], ids=["q4k", "q6k"])
+def test_dequant_bit_exact(ctx, qtype, layout):
+    cols, rows = 1024, 192
+    host, w = weights(qtype, 100 + qtype, rows, cols, layout)
+    out32 = torch.empty((rows - 64, cols), dtype=torch.float32, device="cuda")
+    out16 = torch.empty((rows - 64, cols), dtype=torch.int16, device="cuda")
+    ctx.dequant(w, qtype, layout, cols, rows, 64, rows - 64, out32, out16)
+    torch.cuda.synchronize()
+    want = O.dequant_rows(qtype, O.ROW_MAJOR, host, cols, rows, 64, rows - 64)
+    got32 = out32.cpu().numpy()
+    assert np.array_equal(got32.view(np.uint32), want.view(np.uint32))
+    got16 = out16.cpu().numpy().view(np.uint16)
+    assert np.array_equal(got16, want.astype(np.float16).view(np.uint16))
+
+
+# ---- decode GEMV ----------------------------------------------------------------
+
+GEMV_CASES = [
+    (N.Q4_K, 3840, 15360, "cfg0_q4k_gate"),
+    (N.Q6_K, 15360, 3840, "cfg1a_q6k_down"),
+    (N.Q4_K, 15360, 3840, "q4k_down"),
+    (N.Q6_K, 256, 64, "tiny"),
+    (N.Q4_K, 512, 192, "small"),
+]
+
+
+@pytest.mark.parametrize("layout", LAYOUTS, ids=LNAME.get)
+@pytest.mark.parametrize("qtype,cols,rows,name", GEMV_CASES, ids=[c[3] for c in GEMV_CASES])
+def test_gemv(ctx, qtype, cols, rows, name, layout):
+    host, w = weights(qtype, 7, rows, cols, layout)
+    x = f32(cols, 8)
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    ctx.matmul(w, qtype, layout, cols, rows, 1, torch.from_numpy(x).cuda(), y)
+    torch.cuda.synchronize()
+    ref = O.gemv(qtype, O.ROW_MAJOR, host, cols, rows, x)
+    assert rel_err(y.cpu().numpy(), ref) <= TOL32
+
+
+@pytest.mark.parametrize("layout", [N.CDNA4, N.ROW_MAJOR], ids=LNAME.get)
+def test_lm_head_gemv(ctx, layout):
+    """Config 1b: Q6_K 262144 x 3840 lm-head (row-major in the reference, mm:576)."""
+    cols, rows = 3840, 262144
+    host, w = weights(N.Q6_K, 9, rows, cols, layout)
+    x = f32(cols, 10)
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    ctx.matmul(w, N.Q6_K, layout, cols, rows, 1, torch.from_numpy(x).cuda(), y)
+    torch.cuda.synchronize()
+    ref = O.gemv(N.Q6_K, O.ROW_MAJOR, host, cols, rows, x)
+    assert rel_err(y.cpu().numpy(), ref) <= TOL32
+
+
+def test_gemv_deterministic(ctx):
+    cols, rows = 15360, 3840
+    _, w = weights(N.Q6_K, 11, rows, cols, N.CDNA4)
+    x = torch.from_numpy(f32(cols, 12)).cuda()
+    ys = []
+    for _ in range(3):
+        y = torch.empty(rows, dtype=torch.float32, device="cuda")
+        ctx.matmul(w, N.Q6_K, N.CDNA4, cols, rows, 1, x, y)
+        ys.append(y)
+    torch.cuda.synchronize()
+    assert all(torch.equal(ys[0], t) for t in ys[1:])
+
+
+@pytest.mark.parametrize("layout", LAYOUTS, ids=LNAME.get)
+def test_gate_up_geglu_decode(ctx, layout):
+    cols, rows = 3840, 15360
+    hg, wg = weights(N.Q4_K, 21, rows, cols, layout)
+    hu, wu = weights(N.Q4_K, 22, rows, cols, layout)
+    x = f32(cols, 23)
+    h = torch.empty(rows, dtype=torch.float32, device="cuda")
+    ctx.gate_up_geglu_decode(wg, wu, layout, cols, rows, torch.from_numpy(x).cuda(), h)
+    torch.cuda.synchronize()
+    ref = O.gate_up_geglu(O.ROW_MAJOR, hg, hu, cols, rows, x)
+    assert rel_err(h.cpu().numpy(), ref) <= TOL32
+
+
+def test_ffn_block_decode_two_layers(ctx):
+    """Config 2 for two seeded layers: gate/up+GeGLU then the Q6_K down GEMV,
+    each layer's output compared with the oracle fed the same input."""
+    D, F = 3840, 15360
+    x = f32(D, 31)
+    for layer in range(2):
+        s = N.layer_seed(1000, layer)
+        hg, wg = weights(N.Q4_K, s + 1, F, D, N.CDNA4)
+        hu, wu = weights(N.Q4_K, s + 2, F, D, N.CDNA4)
+        hd, wd = weights(N.Q6_K, s + 3, D, F, N.CDNA4)
+        xd = torch.from_numpy(x).cuda()
+        h = torch.empty(F, dtype=torch.float32, device="cuda")
+        y = torch.empty(D, dtype=torch.float32, device="cuda")
+        ctx.gate_up_geglu_decode(wg, wu, N.CDNA4, D, F, xd, h)
+        ctx.ffn_down(wd, N.Q6_K, N.CDNA4, F, D, 1, h, y, half_input=False, fast_swa=False)
+        torch.cuda.synchronize()
+        h_ref = O.gate_up_geglu(O.ROW_MAJOR, hg, hu, D, F, x)
+        assert rel_err(h.cpu().numpy(), h_ref) <= TOL32
+        y_ref = O.gemv(N.Q6_K, O.ROW_MAJOR, hd, F, D, h.cpu().numpy())
+        yg = y.cpu().numpy()
+        assert rel_err(yg, y_ref) <= TOL32
+        x = (yg / np.sqrt(np.mean(yg.astype(np.float64) ** 2))).astype(np.float32)
+
+
+# ---- prefill GEMM ---------------------------------------------------------------
+
+PREFILL_SMALL = [(512, 128, 5), (1024, 192, 33), (768, 128, 200), (256, 64, 2)]
+
+
+@pytest.mark.parametrize("layout", [N.CDNA4, N.NSMFFN], ids=LNAME.get)
+@pytest.mark.parametrize("acc", [N.ACC_FP32, N.ACC_FP16], ids=["fp32acc", "fp16acc"])
+@pytest.mark.parametrize("cols,rows,batch", PREFILL_SMALL)
+def test_prefill_gate_up_small(ctx, cols, rows, batch, acc, layout):
+    hg, wg = weights(N.Q4_K, 41, rows, cols, layout)
+    hu, wu = weights(N.Q4_K, 42, rows, cols, layout)
+    x = N.synth_normal_f16(43, batch * cols).reshape(batch, cols)
+    h = torch.empty((batch, rows), dtype=torch.int16, device="cuda")
+    ctx.gate_up_geglu_rm32(wg, wu, layout, cols, rows, batch, dev_u16(x), h, fast_swa=(acc == N.ACC_FP16))
+    torch.cuda.synchronize()
+    got = f16_value(h.cpu().numpy().view(np.uint16))
+    ref32 = O.gate_up_geglu_prefill(O.ROW_MAJOR, hg, hu, cols, rows, batch, x, 0)
+    assert rel_err(got, ref32) <= (TOL32 if acc == N.ACC_FP32 else TOL16)
+    if acc == N.ACC_FP16:
+        ref16 = O.gate_up_geglu_prefill(O.ROW_MAJOR, hg, hu, cols, rows, batch, x, 1)
+        assert rel_err(got, ref16) <= 4e-3
+
+
+@pytest.mark.parametrize("layout", [N.CDNA4, N.NSMFFN], ids=LNAME.get)
+@pytest.mark.parametrize("acc", [N.ACC_FP32, N.ACC_FP16], ids=["fp32acc", "fp16acc"])
+@pytest.mark.parametrize("qtype", [N.Q6_K, N.Q4_K], ids=["q6k", "q4k"])
+@pytest.mark.parametrize("cols,rows,batch", PREFILL_SMALL)
+def test_prefill_down_small(ctx, cols, rows, batch, qtype, acc, layout):
+    hw, w = weights(qtype, 51, rows, cols, layout)
+    x = N.synth_normal_f16(52, batch * cols).reshape(batch, cols)
+    y = torch.empty((batch, rows), dtype=torch.float32, device="cuda")
+    ctx.ffn_down(w, qtype, layout, cols, rows, batch, dev_u16(x), y, half_input=True,
+                 fast_swa=(acc == N.ACC_FP16))
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    ref32 = O.gemm(qtype, O.ROW_MAJOR, hw, cols, rows, batch, x, 0)
+    assert rel_err(got, ref32) <= (TOL32 if acc == N.ACC_FP32 else TOL16)
+    if acc == N.ACC_FP16:
+        assert np.array_equal(got, got.astype(np.float16).astype(np.float32))
+        ref16 = O.gemm(qtype, O.ROW_MAJOR, hw, cols, rows, batch, x, 1)
+        assert rel_err(got, ref16) <= 4e-3
+
+
+def _row_slice(host, qtype, cols, r0, nrows):
+    bpr = (cols // 256) * N.BLOCK_BYTES[qtype]
+    return np.ascontiguousarray(host[r0 * bpr:(r0 + nrows) * bpr])
+
+
+@pytest.mark.parametrize("acc", [N.ACC_FP32, N.ACC_FP16], ids=["fp32acc", "fp16acc"])
+def test_prefill_ffn_full_size(ctx, acc):
+    """Config 3 at full size (batch 1024, 3840 -> 15360 -> 3840).  The GPU runs
+    the whole block; the oracle checks 128-row samples of H and of Y (the down
+    check feeds the oracle the GPU's fp16 H, isolating each GEMM)."""
+    D, F, B = 3840, 15360, 1024
+    hg, wg = weights(N.Q4_K, 61, F, D, N.CDNA4)
+    hu, wu = weights(N.Q4_K, 62, F, D, N.CDNA4)
+    hd, wd = weights(N.Q6_K, 63, D, F, N.CDNA4)
+    x = N.synth_normal_f16(64, B * D).reshape(B, D)
+    h = torch.empty((B, F), dtype=torch.int16, device="cuda")
+    y = torch.empty((B, D), dtype=torch.float32, device="cuda")
+    fast = acc == N.ACC_FP16
+    ctx.gate_up_geglu_rm32(wg, wu, N.CDNA4, D, F, B, dev_u16(x), h, fast_swa=fast)
+    ctx.ffn_down(wd, N.Q6_K, N.CDNA4, F, D, B, h, y, half_input=True, fast_swa=fast)
+    torch.cuda.synchronize()
+    hh = h.cpu().numpy().view(np.uint16)
+    yy = y.cpu().numpy()
+    assert np.isfinite(f16_value(hh)).all() and np.isfinite(yy).all()
+    tol = TOL32 if acc == N.ACC_FP32 else TOL16
+    for r0 in (0, 7040, F - 128):
+        ref = O.gate_up_geglu_prefill(O.ROW_MAJOR, _row_slice(hg, N.Q4_K, D, r0, 128),
+                                      _row_slice(hu, N.Q4_K, D, r0, 128), D, 128, B, x, 0)
+        assert rel_err(f16_value(hh[:, r0:r0 + 128]), ref) <= tol
+    for r0 in (0, 1984, D - 128):
+        ref = O.gemm(N.Q6_K, O.ROW_MAJOR, _row_slice(hd, N.Q6_K, F, r0, 128), F, 128, B, hh, 0)
+        assert rel_err(yy[:, r0:r0 + 128], ref) <= tol
+
+
+# ---- device layout conversion and argument errors -------------------------------
+
+@pytest.mark.parametrize("qtype", [N.Q4_K, N.Q6_K], ids=["q4k", "q6k"])
+def test_retile_device_matches_host(ctx, qtype):
+    cols, rows = 768, 192
+    host = N.synth_weights(qtype, 71, rows, cols)
+    src = dev_bytes(host)
+    for to in (N.NSMFFN, N.CDNA4):
+        dst = torch.empty_like(src)
+        N.retile_device(src, dst, qtype, cols, rows, N.ROW_MAJOR, to)
+        torch.cuda.synchronize()
+        assert np.array_equal(dst.cpu().numpy(), N.retile(host, qtype, cols, rows, N.ROW_MAJOR, to))
+
+
+def test_argument_errors(ctx):
+    _, w = weights(N.Q4_K, 81, 64, 256, N.CDNA4)
+    x = torch.zeros(256, dtype=torch.float32, device="cuda")
+    y = torch.zeros(64, dtype=torch.float32, device="cuda")
+    with pytest.raises(N.NsError) as e:
+        ctx.matmul(w, N.Q4_K, N.CDNA4, 300, 64, 1, x, y)
+    assert e.value.code == 2
+    with pytest.raises(N.NsError) as e:
+        ctx.matmul(w[1:], N.Q4_K, N.CDNA4, 256, 64, 1, x, y)
+    assert "misaligned" in str(e.value)
+    with pytest.raises(N.NsError) as e:
+        ctx.gate_up_geglu_rm32(w, w, N.ROW_MAJOR, 256, 64, 8, x, y, False)
+    assert e.value.code == 4

@@ -1,0 +1,211 @@
+"""CPU tests pinning the oracle (oracle/ns_oracle.c) before it is trusted.
+
+Pins, per oracle function:
+  f16<->f32      numpy float16 over all 65536 half patterns / 200k float patterns.
+  q4k/q6k value  the reference's own quant.cpp (oracle/_ref, compiled from the
+                 reference checkout, when present), the committed golden vectors
+                 made from it (tests/golden/), and hand-built closed-form blocks.
+  dot_row        oracle/_ref bit-exact; one-hot columns; linearity.
+  gemv           bit-identical to dot_row for every row.
+  gelu_tanh      gelu(0)=0, gelu(g)-gelu(-g)=g, large |g| -> relu, float64 formula.
+  .nsmffn index  metal_ffn.cpp:145-146 known answers and bijection.
+  FP16 mode      no reference can run (Apple half accumulators): only bounded
+                 against the FP32 mode -- parity unpinned beyond that.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import ns_oracle as O
+from helpers import f16_bits, q4k_block, q6k_block
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "quant_golden.npz")
+
+
+def _rng(seed=1234):
+    return np.random.default_rng(seed)
+
+
+def test_f16_to_f32_all_patterns():
+    L = O.lib()
+    h = np.arange(65536, dtype=np.uint32)
+    got = np.array([L.nso_f16_to_f32(int(v)) for v in h], dtype=np.float32)
+    want = h.astype(np.uint16).view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_rne():
+    L = O.lib()
+    rng = _rng()
+    bits = rng.integers(0, 2**32, size=200_000, dtype=np.uint64).astype(np.uint32)
+    specials = np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 1e-8, 2.0**-25, 2.0**-24, 3 * 2.0**-25,
+                         2.0**-14, 6.1e-5, 1.0 + 2.0**-11, 1.0 + 3 * 2.0**-11, np.inf, -np.inf],
+                        dtype=np.float32).view(np.uint32)
+    f = np.concatenate([bits, specials]).view(np.float32)
+    f = f[~np.isnan(f)]
+    got = np.array([L.nso_f32_to_f16(float(v)) for v in f], dtype=np.uint16)
+    want = f.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def _random_blocks(qtype, n, seed):
+    """Uniform random bytes with sane (finite) fp16 scale fields, plus extremes."""
+    rng = _rng(seed)
+    bs = 144 if qtype == O.Q4_K else 210
+    b = rng.integers(0, 256, size=(n, bs), dtype=np.uint8)
+    scale = rng.choice([1e-3, 0.5, 3.0e-6, 6.0e-8, 0.0, 65504.0], size=(n, 2)).astype(np.float16)
+    if qtype == O.Q4_K:
+        b[:, 0:2] = scale[:, 0:1].view(np.uint8)
+        b[:, 2:4] = scale[:, 1:2].view(np.uint8)
+    else:
+        b[:, 208:210] = scale[:, 0:1].view(np.uint8)
+    return np.ascontiguousarray(b.reshape(-1))
+
+
+@pytest.mark.parametrize("qtype", [O.Q4_K, O.Q6_K])
+def test_values_match_reference_quant_cpp(qtype):
+    if O.ref() is None:
+        pytest.skip("oracle/_ref not built (reference checkout absent); golden vectors cover this")
+    n = 64
+    w = _random_blocks(qtype, n, seed=qtype)
+    cols, rows = 512, n // 2
+    mine = O.dequant_rows(qtype, O.ROW_MAJOR, w, cols, rows).reshape(-1)
+    rc, theirs = O.ref_dequant(qtype, w, cols, rows, 0, cols * rows)
+    assert rc == 0
+    assert np.array_equal(mine.view(np.uint32), theirs.view(np.uint32))
+    x = _rng(7).standard_normal(cols).astype(np.float32)
+    for r in range(rows):
+        rc, d = O.ref_dot_row(qtype, w, cols, rows, r, x)
+        assert rc == 0
+        assert np.float32(d).view(np.uint32) == np.float32(O.dot_row(qtype, O.ROW_MAJOR, w, cols, rows, r, x)).view(np.uint32)
+
+
+def test_reference_rejects_out_of_range():
+    if O.ref() is None:
+        pytest.skip("oracle/_ref not built")
+    w = _random_blocks(O.Q4_K, 2, 3)
+    rc, _ = O.ref_dequant(O.Q4_K, w, 256, 2, 511, 2)  # element 512 is out of range
+    assert rc != 0
+
+
+def test_golden_vectors():
+    g = np.load(GOLDEN, allow_pickle=False)
+    for name, qtype in (("q4k", O.Q4_K), ("q6k", O.Q6_K)):
+        w = np.ascontiguousarray(g[f"{name}_bytes"])
+        cols, rows = int(g[f"{name}_shape"][0]), int(g[f"{name}_shape"][1])
+        want = g[f"{name}_values"].reshape(rows, cols)
+        got = O.dequant_rows(qtype, O.ROW_MAJOR, w, cols, rows)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), name
+        x = g[f"{name}_x"]
+        for r in range(rows):
+            d = O.dot_row(qtype, O.ROW_MAJOR, w, cols, rows, r, x)
+            assert np.float32(d).view(np.uint32) == g[f"{name}_dot"][r].view(np.uint32), (name, r)
+
+
+def test_q4k_closed_forms():
+    # d=1, dmin=0.5, scales sc_g = g+1, mins m_g = 2g, q = element index mod 16
+    sc = [g + 1 for g in range(8)]
+    m = [2 * g for g in range(8)]
+    q = [i % 16 for i in range(256)]
+    b = q4k_block(1.0, 0.5, sc, m, q)
+    vals = np.array([O.lib().nso_q4k_value(b.ctypes.data, i) for i in range(256)], dtype=np.float32)
+    want = np.array([1.0 * sc[i // 32] * q[i] - 0.5 * m[i // 32] for i in range(256)], dtype=np.float32)
+    assert np.array_equal(vals, want)
+    # high-bit scales (sc, m >= 16 exercise the 2-bit tops stored in scales[0..7])
+    b = q4k_block(2.0, 1.0, [63, 17, 32, 48, 63, 17, 32, 48], [63, 0, 16, 47, 31, 62, 1, 33], [15] * 256)
+    v = np.array([O.lib().nso_q4k_value(b.ctypes.data, 32 * g) for g in range(8)], dtype=np.float32)
+    assert list(v) == [2.0 * s * 15 - mm for s, mm in zip([63, 17, 32, 48, 63, 17, 32, 48],
+                                                          [63, 0, 16, 47, 31, 62, 1, 33])]
+    # d = dmin = 0 -> zeros; fp16-subnormal d
+    b = q4k_block(0.0, 0.0, [63] * 8, [63] * 8, [15] * 256)
+    assert all(O.lib().nso_q4k_value(b.ctypes.data, i) == 0.0 for i in range(256))
+    sub = float(np.float16(2.0**-20))
+    b = q4k_block(sub, 0.0, [3] * 8, [0] * 8, [5] * 256)
+    assert O.lib().nso_q4k_value(b.ctypes.data, 77) == np.float32(sub * 15)
+
+
+def test_q6k_closed_forms():
+    v = [i % 64 for i in range(256)]
+    sc = [s - 8 for s in range(16)]
+    b = q6k_block(0.25, sc, v)
+    vals = np.array([O.lib().nso_q6k_value(b.ctypes.data, i) for i in range(256)], dtype=np.float32)
+    want = []
+    for i in range(256):
+        half, p = divmod(i, 128)
+        quarter, l = divmod(p, 32)
+        want.append(0.25 * sc[half * 8 + l // 16 + quarter * 2] * (v[i] - 32))
+    assert np.array_equal(vals, np.array(want, dtype=np.float32))
+    # sc = -32, v = 0 -> d * 1024
+    b = q6k_block(0.5, [-32] * 16, [0] * 256)
+    assert O.lib().nso_q6k_value(b.ctypes.data, 200) == 512.0
+
+
+@pytest.mark.parametrize("qtype", [O.Q4_K, O.Q6_K])
+def test_dot_row_one_hot_and_linearity(qtype):
+    w = _random_blocks(qtype, 8, seed=11)
+    cols, rows = 512, 4
+    deq = O.dequant_rows(qtype, O.ROW_MAJOR, w, cols, rows)
+    for k in (0, 37, 255, 256, 511):
+        e = np.zeros(cols, dtype=np.float32)
+        e[k] = 1.0
+        for r in range(rows):
+            assert O.dot_row(qtype, O.ROW_MAJOR, w, cols, rows, r, e) == deq[r, k]
+    rng = _rng(5)
+    x1, x2 = rng.standard_normal((2, cols)).astype(np.float32)
+    for r in range(rows):
+        a = O.dot_row(qtype, O.ROW_MAJOR, w, cols, rows, r, x1 + x2)
+        b = O.dot_row(qtype, O.ROW_MAJOR, w, cols, rows, r, x1) + O.dot_row(qtype, O.ROW_MAJOR, w, cols, rows, r, x2)
+        scale = np.sum(np.abs(deq[r]) * (np.abs(x1) + np.abs(x2)))
+        assert abs(a - b) <= 1e-5 * scale
+
+
+@pytest.mark.parametrize("qtype", [O.Q4_K, O.Q6_K])
+def test_gemv_equals_dot_row(qtype):
+    w = _random_blocks(qtype, 64 * 4, seed=21)
+    cols, rows = 1024, 64
+    x = _rng(9).standard_normal(cols).astype(np.float32)
+    y = O.gemv(qtype, O.ROW_MAJOR, w, cols, rows, x, nthreads=4)
+    for r in range(rows):
+        assert np.float32(y[r]).view(np.uint32) == np.float32(O.dot_row(qtype, O.ROW_MAJOR, w, cols, rows, r, x)).view(np.uint32)
+
+
+def test_gelu_closed_forms():
+    g = O.gelu_tanh
+    assert g(0.0) == 0.0
+    for v in (0.1, 1.0, 3.5, 20.0):
+        assert abs((g(v) - g(-v)) - v) <= 4e-7 * max(1.0, v)
+    assert g(30.0) == 30.0 and g(-30.0) == 0.0
+    xs = np.linspace(-8, 8, 161)
+    ref = 0.5 * xs * (1 + np.tanh(np.sqrt(2 / np.pi) * (xs + 0.044715 * xs**3)))
+    got = np.array([g(float(v)) for v in xs])
+    assert np.max(np.abs(got - ref)) <= 2e-6 * np.max(np.abs(ref))
+
+
+def test_nsmffn_block_index():
+    L = O.lib()
+    # metal_ffn.cpp:145-146: target = ((row0/64)*blocks + block)*64 + row
+    assert L.nso_block_index(O.NSMFFN, 0, 0, 15) == 0
+    assert L.nso_block_index(O.NSMFFN, 1, 0, 15) == 1
+    assert L.nso_block_index(O.NSMFFN, 0, 1, 15) == 64
+    assert L.nso_block_index(O.NSMFFN, 65, 2, 15) == (1 * 15 + 2) * 64 + 1
+    assert L.nso_block_index(O.ROW_MAJOR, 65, 2, 15) == 65 * 15 + 2
+    nb, rows = 3, 128
+    idx = {L.nso_block_index(O.NSMFFN, r, b, nb) for r in range(rows) for b in range(nb)}
+    assert idx == set(range(rows * nb))
+
+
+def test_fp16_mode_oracle_is_fp16_and_close():
+    rng = _rng(3)
+    cols, rows, batch = 512, 64, 5
+    w = _random_blocks(O.Q4_K, rows * cols // 256, seed=4)
+    # keep scales at the model's magnitude so fp16 cannot overflow
+    wb = w.reshape(-1, 144)
+    wb[:, 0:4] = np.array([1e-3, 1e-3], dtype=np.float16).view(np.uint8)
+    x = f16_bits(rng.standard_normal((batch, cols)).astype(np.float16))
+    y32 = O.gemm(O.Q4_K, O.ROW_MAJOR, w, cols, rows, batch, x, 0)
+    y16 = O.gemm(O.Q4_K, O.ROW_MAJOR, w, cols, rows, batch, x, 1)
+    assert np.array_equal(y16, y16.astype(np.float16).astype(np.float32))
+    assert np.max(np.abs(y16 - y32)) <= 4e-3 * np.max(np.abs(y32))
