@@ -46,8 +46,9 @@ enum { NS_LAYOUT_ROW_MAJOR = 0, NS_LAYOUT_NSMFFN = 1, NS_LAYOUT_CDNA4 = 2 };
 
 /* Accumulation mode of the prefill GEMMs (mm:565 `fast_swa_ffn`).
  *   FP32  fp32 accumulation (the 8 global layers, and every layer with --exact-ffn).
- *   FP16  the local-layer mode: the running fp32 sum is rounded to fp16 at every
- *         256-wide super-block boundary and the result is fp16. */
+ *   FP16  the local-layer mode: the running fp32 sum is rounded to fp16
+ *         precision (11 significant bits, round to nearest even, fp32 exponent
+ *         range) at every 256-wide super-block boundary. */
 enum { NS_ACC_FP32 = 0, NS_ACC_FP16 = 1 };
 
 enum { NS_OK = 0, NS_ERR_ARG = 1, NS_ERR_SHAPE = 2, NS_ERR_HIP = 3, NS_ERR_UNSUPPORTED = 4 };

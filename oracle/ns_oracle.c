@@ -58,7 +58,17 @@ uint16_t nso_f32_to_f16(float f) {
     return sign | (uint16_t)r;
 }
 
-static float round_f16(float v) { return nso_f16_to_f32(nso_f32_to_f16(v)); }
+/* FP16-mode rounding: round to nearest even at 11 significant bits (the fp16
+ * significand) while keeping the fp32 exponent range, so values beyond the
+ * fp16 maximum do not overflow.  Equals fp16 rounding on the fp16 normal range. */
+float nso_round_f16p(float v) {
+    uint32_t b;
+    memcpy(&b, &v, 4);
+    if ((b & 0x7f800000u) == 0x7f800000u) return v;
+    b = (b + 0x0fffu + ((b >> 13) & 1u)) & 0xffffe000u;
+    memcpy(&v, &b, 4);
+    return v;
+}
 
 /* ---- element values (quant.cpp:9-18) ------------------------------------ */
 
@@ -189,7 +199,7 @@ static void *gemm_worker(void *p) {
             const float *xk = j->xt + k * B;
             for (uint64_t t = 0; t < B; ++t) acc[t] += wk * xk[t];
             if (j->acc_mode == 1 && (k % 256) == 255)
-                for (uint64_t t = 0; t < B; ++t) acc[t] = round_f16(acc[t]);
+                for (uint64_t t = 0; t < B; ++t) acc[t] = nso_round_f16p(acc[t]);
         }
         for (uint64_t t = 0; t < B; ++t) j->out[t * j->rows + r] = acc[t];
     }
@@ -250,8 +260,8 @@ int nso_gemm(int type, int layout, const uint8_t *w, uint64_t cols, uint64_t row
     j.rows = rows; j.batch = batch; j.xt = xt; j.out = out;
     run_rows(&j, rows, nthreads, gemm_worker);
     free(xt);
-    if (acc_mode == 1) /* FP16 mode: outputs are fp16 values (metal:394, :489 widen half) */
-        for (uint64_t i = 0; i < rows * batch; ++i) out[i] = round_f16(out[i]);
+    if (acc_mode == 1) /* FP16 mode: outputs carry fp16 precision (metal:394, :489 widen half) */
+        for (uint64_t i = 0; i < rows * batch; ++i) out[i] = nso_round_f16p(out[i]);
     return 0;
 }
 

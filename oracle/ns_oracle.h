@@ -20,6 +20,7 @@
  *     committed golden vectors from it, closed-form hand-built blocks.
  *   dot_row: oracle/_ref dot_row bit-exact, linearity and one-hot columns.
  *   gelu_tanh: closed forms (gelu(0)=0, large |g| -> relu, odd part identity).
+ *   round_f16p: equals numpy float16 rounding over the fp16 normal range.
  *   FP16-accumulation mode (nso_gemm acc_mode=1): parity unpinned -- the
  *     reference's Apple simdgroup_half8x8 rounding cannot run here; it is
  *     checked only against the fp32 path within the 1e-2 tolerance.
@@ -38,6 +39,8 @@ enum { NSO_ROW_MAJOR = 0, NSO_NSMFFN = 1, NSO_CDNA4 = 2 };
 
 float nso_f16_to_f32(uint16_t h);
 uint16_t nso_f32_to_f16(float f);
+/* Round to 11 significant bits (RNE), fp32 exponent range: the FP16 mode's rounding. */
+float nso_round_f16p(float v);
 
 float nso_q4k_value(const uint8_t *block, uint32_t i);
 float nso_q6k_value(const uint8_t *block, uint32_t i);
@@ -67,7 +70,8 @@ int nso_gate_up_geglu(int layout, const uint8_t *wg, const uint8_t *wu, uint64_t
 /* Prefill contraction: out[t][r] = sum_k W[r][k] * x[t][k] for t < batch.
  * x is fp16 bits [batch][cols].  acc_mode 0 = FP32 (sequential fp32 sum, fp32 out);
  * acc_mode 1 = FP16 mode as defined by this build: the fp32 running sum is
- * rounded to fp16 at every 256-wide super-block boundary and the result is fp16. */
+ * rounded to fp16 precision (nso_round_f16p) at every 256-wide super-block
+ * boundary, so the result carries fp16 precision (without fp16's overflow). */
 int nso_gemm(int type, int layout, const uint8_t *w, uint64_t cols, uint64_t rows,
              uint64_t batch, const uint16_t *x_f16, int acc_mode, float *out, int nthreads);
 

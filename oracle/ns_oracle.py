@@ -30,6 +30,8 @@ def lib():
         L.nso_f16_to_f32.restype = f32
         L.nso_f32_to_f16.argtypes = [f32]
         L.nso_f32_to_f16.restype = ctypes.c_uint16
+        L.nso_round_f16p.argtypes = [f32]
+        L.nso_round_f16p.restype = f32
         L.nso_q4k_value.argtypes = [vp, ctypes.c_uint32]
         L.nso_q4k_value.restype = f32
         L.nso_q6k_value.argtypes = [vp, ctypes.c_uint32]

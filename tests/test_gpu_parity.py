@@ -192,7 +192,7 @@ def test_prefill_down_small(ctx, cols, rows, batch, qtype, acc, layout):
     ref32 = O.gemm(qtype, O.ROW_MAJOR, hw, cols, rows, batch, x, 0)
     assert rel_err(got, ref32) <= (TOL32 if acc == N.ACC_FP32 else TOL16)
     if acc == N.ACC_FP16:
-        assert np.array_equal(got, got.astype(np.float16).astype(np.float32))
+        assert not np.any(got.view(np.uint32) & 0x1FFF)  # fp16 precision: 11 significant bits
         ref16 = O.gemm(qtype, O.ROW_MAJOR, hw, cols, rows, batch, x, 1)
         assert rel_err(got, ref16) <= 4e-3
 

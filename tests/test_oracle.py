@@ -207,5 +207,20 @@ def test_fp16_mode_oracle_is_fp16_and_close():
     x = f16_bits(rng.standard_normal((batch, cols)).astype(np.float16))
     y32 = O.gemm(O.Q4_K, O.ROW_MAJOR, w, cols, rows, batch, x, 0)
     y16 = O.gemm(O.Q4_K, O.ROW_MAJOR, w, cols, rows, batch, x, 1)
-    assert np.array_equal(y16, y16.astype(np.float16).astype(np.float32))
+    assert not np.any(y16.view(np.uint32) & 0x1FFF)  # 11 significant bits
     assert np.max(np.abs(y16 - y32)) <= 4e-3 * np.max(np.abs(y32))
+
+
+def test_round_f16p():
+    """FP16-mode rounding equals fp16 RNE on the fp16 normal range and keeps
+    magnitudes beyond it (no overflow)."""
+    L = O.lib()
+    rng = _rng(8)
+    v = (rng.standard_normal(50_000) * np.exp(rng.uniform(-9, 11, 50_000))).astype(np.float32)
+    v = v[(np.abs(v) >= 2.0**-14) & (np.abs(v) < 65504)]
+    got = np.array([L.nso_round_f16p(float(a)) for a in v], dtype=np.float32)
+    assert np.array_equal(got, v.astype(np.float16).astype(np.float32))
+    big = np.float32(171474.9)
+    r = L.nso_round_f16p(float(big))
+    assert np.isfinite(r) and abs(r - big) <= big * 2.0**-11
+    assert L.nso_round_f16p(1.0 + 2.0**-11) == 1.0 and L.nso_round_f16p(1.0 + 3 * 2.0**-11) == 1.0 + 2.0**-9
