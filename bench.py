@@ -184,12 +184,18 @@ def main():
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import ns_oracle as O
 
+        # repeat whole config-1 steps until at least 10 s of CPU time have passed
+        reps = 0
         t = time.perf_counter()
-        ref_dn = O.gemv(N.Q6_K, O.ROW_MAJOR, down_host0, F, D, x_dn_h, nthreads=nthreads)
-        ref_lm = O.gemv(N.Q6_K, O.ROW_MAJOR, lm_host, D, V, x_lm_h, nthreads=nthreads)
-        dt = time.perf_counter() - t
-        cpu = {"value": round(bytes_step / dt / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
-               "sample": "one full config-1 step (Q6_K down 3840x15360 + lm-head 262144x3840 GEMV) by the "
+        while True:
+            ref_dn = O.gemv(N.Q6_K, O.ROW_MAJOR, down_host0, F, D, x_dn_h, nthreads=nthreads)
+            ref_lm = O.gemv(N.Q6_K, O.ROW_MAJOR, lm_host, D, V, x_lm_h, nthreads=nthreads)
+            reps += 1
+            dt = time.perf_counter() - t
+            if dt >= 10.0 or reps >= 200:
+                break
+        cpu = {"value": round(reps * bytes_step / dt / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
+               "sample": f"{reps} full config-1 steps (Q6_K down 3840x15360 + lm-head 262144x3840 GEMV) by the "
                          f"oracle's dequant-once sequential-fp32 dot, {dt:.2f} s on {cpu_model()}"}
         # the same inputs on the GPU: a free parity check of the measured kernels
         ctx.matmul(downs[0], N.Q6_K, N.CDNA4, F, D, 1, x_dn, y_dn)

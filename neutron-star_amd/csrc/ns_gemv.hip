@@ -245,24 +245,35 @@ __global__ __launch_bounds__(kMaxWaves * 64) void gemv_kernel(
         if constexpr (PAIR) s1 += red[PAIR ? 1 : 0][w][lane];
     }
     if (kchunks > 1) {
+        // Hand-off between workgroups through device-coherent (agent-scope)
+        // atomic stores and loads only: the partials bypass the XCD-private L2,
+        // so no L2-wide write-back/invalidate fence is needed.  The wait below
+        // makes every partial store complete before the arrival is counted;
+        // the last arrival reads them after its counter atomic has returned.
         if (valid) {
-            partial[size_t(kc) * rows + row] = s0;
-            if constexpr (PAIR) partial[size_t(kchunks + kc) * rows + row] = s1;
+            __hip_atomic_store(&partial[size_t(kc) * rows + row], s0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if constexpr (PAIR)
+                __hip_atomic_store(&partial[size_t(kchunks + kc) * rows + row], s1, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
         }
-        __threadfence();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
         uint32_t prev = 0;
-        if (lane == 0) prev = atomicAdd(&counters[slab], 1u);
+        if (lane == 0)
+            prev = __hip_atomic_fetch_add(&counters[slab], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         prev = __shfl(prev, 0);
         if (prev != kchunks - 1) return;
-        __threadfence();
         s0 = 0.f;
         s1 = 0.f;
         if (valid)
             for (uint32_t k = 0; k < kchunks; ++k) {
-                s0 += __builtin_nontemporal_load(&partial[size_t(k) * rows + row]);
-                if constexpr (PAIR) s1 += __builtin_nontemporal_load(&partial[size_t(kchunks + k) * rows + row]);
+                s0 += __hip_atomic_load(&partial[size_t(k) * rows + row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if constexpr (PAIR)
+                    s1 += __hip_atomic_load(&partial[size_t(kchunks + k) * rows + row], __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
             }
-        if (lane == 0) atomicExch(&counters[slab], 0u);
+        if (lane == 0) __hip_atomic_store(&counters[slab], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (!valid) return;
     if constexpr (PAIR) out[row] = gelu_tanh(s0) * s1;
