@@ -83,7 +83,9 @@ int gemm(ns_ctx *ctx, const char *fn, int type, int layout, int acc, const void 
          const uint16_t *x, void *out, uint32_t cols, uint32_t rows, uint32_t batch, hipStream_t s) {
     if (layout == ROW_MAJOR)
         return fail(NS_ERR_UNSUPPORTED, std::string(fn) + ": the prefill GEMM needs the NSMFFN or CDNA4 slab layout");
-    if (int rc = ensure_ws(ctx, gemm_workspace_floats(type, cols, batch), 0)) return rc;
+    size_t wf = 0, wc = 0;
+    gemm_workspace_need(type, cols, rows, batch, up != nullptr, &wf, &wc);
+    if (int rc = ensure_ws(ctx, wf, wc)) return rc;
     const hipError_t e = launch_gemm(type, layout, acc, static_cast<const uint8_t *>(w),
                                      static_cast<const uint8_t *>(up), x, out, cols, rows, batch, ctx->ws, s);
     return e == hipSuccess ? NS_OK : hip_fail(e, fn);

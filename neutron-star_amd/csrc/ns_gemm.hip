@@ -37,6 +37,8 @@
 //         range) after every super-block update, so outputs carry fp16
 //         precision (metal:394/:489 widen half tiles).  True fp16 range would
 //         overflow on BASELINE's synthetic inputs (down outputs reach 1.7e5).
+#include <type_traits>
+
 #include "ns_internal.hpp"
 #include "ns_quant.hpp"
 
@@ -46,11 +48,17 @@ namespace {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
-constexpr int TT = 128;        // tokens per workgroup tile
-constexpr int TC = 128;        // B columns per workgroup tile
+constexpr int TT = 256;        // tokens per workgroup tile
+constexpr int TC = 256;        // B columns per workgroup tile
+constexpr int kWaves = 8;      // 2 (tokens) x 4 (columns)
+constexpr int kThreads = 64 * kWaves;
+constexpr int WT = 128;        // tokens per wave
+constexpr int WC = 64;         // B columns per wave
+constexpr int MI = WT / 32;    // 32x32 MFMA tiles per wave along tokens
+constexpr int NJ = WC / 32;    // ... along columns
 constexpr int KS = 64;         // k per step
-constexpr int LDSW = KS + 8;   // padded LDS row (halfs)
-constexpr int kThreads = 256;
+constexpr int LDSW = KS + 8;   // padded LDS row of the weight tile (halfs)
+constexpr int XDMA = TT * KS * 2 / 16 / kThreads;  // 16-byte x chunks each thread moves per step
 
 // FP16-mode rounding: nearest even at 11 significant bits (the fp16
 // significand), fp32 exponent range.  Identical to fp16 rounding on the fp16
@@ -64,291 +72,440 @@ __device__ __forceinline__ float round_f16p(float v) {
 __device__ __forceinline__ half2_t h2(uint32_t bits) { return __builtin_bit_cast(half2_t, bits); }
 __device__ __forceinline__ uint32_t u32(half2_t v) { return __builtin_bit_cast(uint32_t, v); }
 
-// Two small unsigned fields (selected bytes of w, masked) as fp16 1024+f
-// (0x6400 | f): v_perm spreads bytes into the two 16-bit lanes.
+// Two small unsigned fields (selected bytes of w, masked) as fp16 1024+f: one
+// v_perm places bytes b_i of w under 0x64 exponent bytes, one AND keeps the field.
 __device__ __forceinline__ half2_t magic_pair(uint32_t w, uint32_t sel, uint32_t mask) {
-    return h2((__builtin_amdgcn_perm(w, w, sel) & mask) | 0x64006400u);
+    return h2(__builtin_amdgcn_perm(0x64646464u, w, sel) & mask);
 }
-constexpr uint32_t kSel01 = 0x0c010c00u;  // [0, b1, 0, b0]
-constexpr uint32_t kSel23 = 0x0c030c02u;  // [0, b3, 0, b2]
+constexpr uint32_t kSel01 = 0x04010400u;  // [0x64, b1, 0x64, b0]
+constexpr uint32_t kSel23 = 0x04030402u;  // [0x64, b3, 0x64, b2]
+constexpr uint32_t kMask4 = 0xFF0FFF0Fu;
+constexpr uint32_t kMask6 = 0xFF3FFF3Fu;
 
 // sc*(1024+f) + bias with one rounding; exact because the result is an integer <= 2048.
 __device__ __forceinline__ uint32_t scale_pair(half2_t t, half2_t sc, half2_t bias) {
     return u32(__builtin_elementwise_fma(t, sc, bias));
 }
 
+// Buffer-resource loads: bounds-checked by the descriptor (reads at or past
+// `bytes` return 0), so no per-lane branch guards a load.  A guarded load would
+// make the compiler wait for it at once, defeating the prefetch below.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, int(bytes), 0x00020000);
+}
+__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, int(off), 0, 0);
+}
+__device__ __forceinline__ uint32_t bload2(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, int(off), 0, 0);
+}
+
 struct WRun {
     u32x4 v[4];  // v[0..1]: 16 halfs at k offset k_lo, v[2..3]: 16 halfs at k_hi
-    int k_lo, k_hi;
 };
 
-// Q4_K producer.  Step s covers groups 2p, 2p+1 (p = s%4) of super-block s/4:
-// qs bytes 32p..32p+31, low nibble -> group 2p, high -> group 2p+1.  Thread
-// half hh takes bytes 32p+16hh..+15: run 0 = group 2p, l = 16hh..+15 (k offset
-// 16hh); run 1 = group 2p+1, same l (k offset 32+16hh).  Values: sc_g * q.
+// Raw bytes one producer thread loads for one k step.
+struct RawQ4 {
+    u32x4 hdr, qs;
+};
+struct RawQ6 {
+    u32x4 ql[2], qh[2], scw;
+    uint32_t dbits;
+};
+template <int TYPE>
+using Raw = typename std::conditional<TYPE == Q4_K, RawQ4, RawQ6>::type;
+
+// Q4_K step s covers groups 2p, 2p+1 (p = s%4) of super-block s/4: qs bytes
+// 32p..32p+31, low nibble -> group 2p, high -> group 2p+1.  Thread half hh
+// takes bytes 32p+16hh..+15: run 0 = group 2p, l = 16hh..+15 (k offset 16hh);
+// run 1 = group 2p+1, same l (k offset 32+16hh).
 template <int LAYOUT>
-__device__ __forceinline__ void q4_tile(const uint8_t *__restrict__ w, uint32_t row, uint32_t nb, uint32_t s,
-                                        uint32_t hh, WRun &out, u32x4 &hdr) {
+__device__ __forceinline__ void load_raw(rsrc_t w, uint32_t row, uint32_t nb, uint32_t s, uint32_t hh, RawQ4 &r) {
     const uint32_t b = s >> 2, p = s & 3;
-    u32x4 qs;
     if constexpr (LAYOUT == CDNA4) {
-        const u32x4 *base = reinterpret_cast<const u32x4 *>(w + region_offset(Q4_K, row / kRowTile, b, nb)) +
-                            (row % kRowTile);
-        hdr = base[0];
-        qs = base[(1 + 2 * p + hh) * kRowTile];
+        const uint32_t base = uint32_t(region_offset(Q4_K, row / kRowTile, b, nb)) + (row % kRowTile) * 16;
+        r.hdr = bload16(w, base);
+        r.qs = bload16(w, base + (1 + 2 * p + hh) * kRowTile * 16);
     } else {
-        const u32x4 *blk = reinterpret_cast<const u32x4 *>(w + block_index(NSMFFN, row, b, nb) * kQ4Bytes);
-        hdr = blk[0];
-        qs = blk[1 + 2 * p + hh];
+        const uint32_t blk = uint32_t(block_index(NSMFFN, row, b, nb)) * kQ4Bytes;
+        r.hdr = bload16(w, blk);
+        r.qs = bload16(w, blk + (1 + 2 * p + hh) * 16);
     }
-    const Q4Scales sc = q4_scales(hdr.y, hdr.z, hdr.w);
-    const _Float16 s0 = _Float16(float(q4_sc(sc, int(2 * p)))), s1 = _Float16(float(q4_sc(sc, int(2 * p + 1))));
+}
+
+// Values: sc_g * q, exact in fp16.
+// z scales the tile: 1 normally (values exact), 0 for d == 0, d/e < 1 for the
+// rare blocks whose d is far below dmin (then rounded; see the kernel comment).
+__device__ __forceinline__ void decode(const RawQ4 &r, uint32_t s, uint32_t hh, float z, WRun &out) {
+    (void)hh;
+    const uint32_t p = s & 3;
+    const Q4Scales sc = q4_scales(r.hdr.y, r.hdr.z, r.hdr.w);
+    const _Float16 s0 = _Float16(z * float(q4_sc(sc, int(2 * p)))), s1 = _Float16(z * float(q4_sc(sc, int(2 * p + 1))));
     const half2_t sc0 = {s0, s0}, sc1 = {s1, s1};
     const half2_t nb0 = {_Float16(-1024.f) * s0, _Float16(-1024.f) * s0};
     const half2_t nb1 = {_Float16(-1024.f) * s1, _Float16(-1024.f) * s1};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t wv = qs[i], wh = wv >> 4;
-        out.v[i >> 1][(i & 1) * 2 + 0] = scale_pair(magic_pair(wv, kSel01, 0x000F000Fu), sc0, nb0);
-        out.v[i >> 1][(i & 1) * 2 + 1] = scale_pair(magic_pair(wv, kSel23, 0x000F000Fu), sc0, nb0);
-        out.v[2 + (i >> 1)][(i & 1) * 2 + 0] = scale_pair(magic_pair(wh, kSel01, 0x000F000Fu), sc1, nb1);
-        out.v[2 + (i >> 1)][(i & 1) * 2 + 1] = scale_pair(magic_pair(wh, kSel23, 0x000F000Fu), sc1, nb1);
+        const uint32_t wv = r.qs[i], wh = wv >> 4;
+        out.v[i >> 1][(i & 1) * 2 + 0] = scale_pair(magic_pair(wv, kSel01, kMask4), sc0, nb0);
+        out.v[i >> 1][(i & 1) * 2 + 1] = scale_pair(magic_pair(wv, kSel23, kMask4), sc0, nb0);
+        out.v[2 + (i >> 1)][(i & 1) * 2 + 0] = scale_pair(magic_pair(wh, kSel01, kMask4), sc1, nb1);
+        out.v[2 + (i >> 1)][(i & 1) * 2 + 1] = scale_pair(magic_pair(wh, kSel23, kMask4), sc1, nb1);
     }
-    out.k_lo = 16 * int(hh);
-    out.k_hi = 32 + 16 * int(hh);
 }
 
-__device__ __forceinline__ u32x4 load_chunk_q6(const uint8_t *__restrict__ blk, uint32_t chunk) {
-    // NSMFFN Q6_K blocks are 2-byte aligned only
-    const uint16_t *h = reinterpret_cast<const uint16_t *>(blk) + 8 * chunk;
-    return u32x4{h[0] | (uint32_t(h[1]) << 16), h[2] | (uint32_t(h[3]) << 16), h[4] | (uint32_t(h[5]) << 16),
-                 h[6] | (uint32_t(h[7]) << 16)};
+__device__ __forceinline__ uint32_t k_lo(int type, uint32_t hh) { return type == Q4_K ? 16 * hh : 32 * hh; }
+__device__ __forceinline__ uint32_t k_hi(int type, uint32_t hh) { return type == Q4_K ? 32 + 16 * hh : 32 * hh + 16; }
+
+// NSMFFN Q6_K blocks are only 2-byte aligned: assemble a 16-byte chunk from halves.
+__device__ __forceinline__ u32x4 load_chunk_q6(rsrc_t w, uint32_t blk, uint32_t chunk) {
+    u32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        v[i] = bload2(w, blk + 16 * chunk + 4 * i) | (bload2(w, blk + 16 * chunk + 4 * i + 2) << 16);
+    return v;
 }
 
-// Q6_K producer.  Step s covers elements 64*(s%4)..+63 of super-block s/4:
-// half h = (s%4)/2, quarters 2*(s%2) and 2*(s%2)+1.  Thread half hh takes
-// quarter qa = 2*(s%2)+hh, l = 0..31 (k offsets 32hh..32hh+31):
+// Q6_K step s covers elements 64*(s%4)..+63 of super-block s/4: half
+// h = (s%4)/2, quarters 2*(s%2) and 2*(s%2)+1.  Thread half hh takes quarter
+// qa = 2*(s%2)+hh, l = 0..31 (k offsets 32hh..32hh+31):
 //   v = nibble of ql[64h + 32*(qa&1) + l] (low if qa < 2) | (qh[32h + l] >> 2qa & 3) << 4.
-// Values: sc * (v - 32), sc = scales[8h + 2qa + l/16].
 template <int LAYOUT>
-__device__ __forceinline__ void q6_tile(const uint8_t *__restrict__ w, uint32_t row, uint32_t nb, uint32_t s,
-                                        uint32_t hh, WRun &out, uint32_t &dbits) {
+__device__ __forceinline__ void load_raw(rsrc_t w, uint32_t row, uint32_t nb, uint32_t s, uint32_t hh, RawQ6 &r) {
     const uint32_t b = s >> 2, sr = s & 3, h = sr >> 1, qa = 2 * (sr & 1) + hh;
-    u32x4 ql[2], qh[2], scw;
     const uint32_t cl = 4 * h + 2 * (qa & 1), chh = 8 + 2 * h;
     if constexpr (LAYOUT == CDNA4) {
-        const uint8_t *reg = w + region_offset(Q6_K, row / kRowTile, b, nb);
-        const u32x4 *base = reinterpret_cast<const u32x4 *>(reg) + (row % kRowTile);
-        ql[0] = base[cl * kRowTile];
-        ql[1] = base[(cl + 1) * kRowTile];
-        qh[0] = base[chh * kRowTile];
-        qh[1] = base[(chh + 1) * kRowTile];
-        scw = base[12 * kRowTile];
-        dbits = reinterpret_cast<const uint16_t *>(reg + kQ6Chunks * 1024)[row % kRowTile];
+        const uint32_t reg = uint32_t(region_offset(Q6_K, row / kRowTile, b, nb));
+        const uint32_t base = reg + (row % kRowTile) * 16;
+        r.ql[0] = bload16(w, base + cl * kRowTile * 16);
+        r.ql[1] = bload16(w, base + (cl + 1) * kRowTile * 16);
+        r.qh[0] = bload16(w, base + chh * kRowTile * 16);
+        r.qh[1] = bload16(w, base + (chh + 1) * kRowTile * 16);
+        r.scw = bload16(w, base + 12 * kRowTile * 16);
+        r.dbits = bload2(w, reg + kQ6Chunks * 1024 + (row % kRowTile) * 2);
     } else {
-        const uint8_t *blk = w + block_index(NSMFFN, row, b, nb) * kQ6Bytes;
-        ql[0] = load_chunk_q6(blk, cl);
-        ql[1] = load_chunk_q6(blk, cl + 1);
-        qh[0] = load_chunk_q6(blk, chh);
-        qh[1] = load_chunk_q6(blk, chh + 1);
-        scw = load_chunk_q6(blk, 12);
-        dbits = reinterpret_cast<const uint16_t *>(blk)[104];
+        const uint32_t blk = uint32_t(block_index(NSMFFN, row, b, nb)) * kQ6Bytes;
+        r.ql[0] = load_chunk_q6(w, blk, cl);
+        r.ql[1] = load_chunk_q6(w, blk, cl + 1);
+        r.qh[0] = load_chunk_q6(w, blk, chh);
+        r.qh[1] = load_chunk_q6(w, blk, chh + 1);
+        r.scw = load_chunk_q6(w, blk, 12);
+        r.dbits = bload2(w, blk + 208);
     }
+}
+
+// Values: sc * (v - 32), sc = scales[8h + 2qa + l/16], exact in fp16.
+__device__ __forceinline__ void decode(const RawQ6 &r, uint32_t s, uint32_t hh, float z, WRun &out) {
+    const uint32_t sr = s & 3, h = sr >> 1, qa = 2 * (sr & 1) + hh;
     const uint32_t si = 8 * h + 2 * qa;
     const uint32_t nshift = qa >= 2 ? 4 : 0, hshift = 2 * qa;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {  // l = 16c .. 16c+15
-        const _Float16 s16 = _Float16(float(int8_t(byte_of(scw[(si + c) >> 2], int((si + c) & 3)))));
+        const _Float16 s16 = _Float16(z * float(int8_t(byte_of(r.scw[(si + c) >> 2], int((si + c) & 3)))));
         const half2_t sc2 = {s16, s16};
         const half2_t nb2 = {_Float16(-1056.f) * s16, _Float16(-1056.f) * s16};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {  // l = 16c + 4i .. +3
-            const uint32_t v = ((ql[c][i] >> nshift) & 0x0F0F0F0Fu) | (((qh[c][i] >> hshift) & 0x03030303u) << 4);
-            out.v[2 * c + (i >> 1)][(i & 1) * 2 + 0] = scale_pair(magic_pair(v, kSel01, 0x003F003Fu), sc2, nb2);
-            out.v[2 * c + (i >> 1)][(i & 1) * 2 + 1] = scale_pair(magic_pair(v, kSel23, 0x003F003Fu), sc2, nb2);
+            const uint32_t v = ((r.ql[c][i] >> nshift) & 0x0F0F0F0Fu) | (((r.qh[c][i] >> hshift) & 0x03030303u) << 4);
+            out.v[2 * c + (i >> 1)][(i & 1) * 2 + 0] = scale_pair(magic_pair(v, kSel01, kMask6), sc2, nb2);
+            out.v[2 * c + (i >> 1)][(i & 1) * 2 + 1] = scale_pair(magic_pair(v, kSel23, kMask6), sc2, nb2);
         }
     }
-    out.k_lo = 32 * int(hh);
-    out.k_hi = 32 * int(hh) + 16;
 }
 
+// Running sum in one accumulator.  Within super-block sb the MFMA accumulator
+// holds S/e_sb, where S is the running sum of the output and e_sb is a per-row
+// factor: e = d for Q6_K; e = max(d, dmin/1024) for Q4_K (e = 1 if that is 0).
+// The tile holds z*sc*q with z = d/e, i.e. the exact integers sc*q whenever
+// e = d; the rare Q4_K blocks with d < dmin/1024 get z < 1 (rounded in fp16,
+// an error on a term at most ~1e-3 of the block's own min term).  The Q4_K
+// min term -dmin/e * sum_g m_g S_g(x) is one more MFMA accumulating into the
+// same registers: A = the group sums of x split into fp16 hi (k 0..7) and lo
+// (k 8..15), B = fp16(-dmin/e * m_g) (|.| <= 1024*63; rounding it costs < 3e-4
+// of a term that is a few percent of the output).  Entering super-block sb+1
+// multiplies the accumulator by e_sb / e_sb+1.
+//
+// Pipeline, per 64-wide k step s (one barrier per step):
+//   decode raw(s) into LDS weight buffer s&1 (raw(s) was loaded two steps ago);
+//   wait for the LDS-DMA of x(s) (issued one step ago); barrier;
+//   issue the LDS-DMA of x(s+1) into x buffer (s+1)&1 and the loads of raw(s+2);
+//   MFMAs on buffers s&1.
+// Buffers written at step s were last read by MFMAs of step s-2 (weights) or
+// s-1 (x), which every wave finished before it passed barrier s-1 or s.
+// x rows are unpadded (128 bytes) with 16-byte chunk c of row R stored at
+// position c ^ ((R >> 1) & 7), which keeps 16 consecutive rows' fragment reads
+// on distinct LDS banks; weight rows are padded to 72 halfs for the same reason.
+//
+// Split K (gridDim.y > 1): workgroup y covers super-blocks [y*nb/Y, (y+1)*nb/Y);
+// each writes its S tile to the workspace, and the last workgroup of a tile to
+// arrive (counted with a device-scope atomic) adds the parts in y order and
+// runs the epilogue, so results do not depend on arrival order.  The hand-off
+// uses device-coherent atomic stores/loads only (no L2-wide fences).
 template <int TYPE, int LAYOUT, int ACC, bool PAIR>
-__global__ __launch_bounds__(kThreads, 2) void gemm_kernel(
+__global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, const uint16_t *__restrict__ x,
-    const uint16_t *__restrict__ xs_hi, const uint16_t *__restrict__ xs_lo, void *__restrict__ out,
-    uint32_t cols, uint32_t rows, uint32_t batch, uint32_t ntok_tiles) {
-    __shared__ __attribute__((aligned(16))) _Float16 Xs[TT * LDSW];
-    __shared__ __attribute__((aligned(16))) _Float16 Ws[TC * LDSW];
-    __shared__ float colD[TC];
-    __shared__ float colDmin[TYPE == Q4_K ? TC : 1];
-    __shared__ __attribute__((aligned(16))) _Float16 colM[TYPE == Q4_K ? TC * 8 : 8];
+    const uint16_t *__restrict__ xsums, void *__restrict__ out, float *__restrict__ partial,
+    uint32_t *__restrict__ counters, uint32_t cols, uint32_t rows, uint32_t batch, uint32_t ntok_tiles,
+    uint32_t wbytes) {
+    constexpr bool Q4 = TYPE == Q4_K;
+    constexpr uint32_t kRawLoads = Q4 ? 2 : (LAYOUT == CDNA4 ? 6 : 41);  // vector loads per load_raw
+    __shared__ __attribute__((aligned(16))) _Float16 Ws[2][TC * LDSW];
+    __shared__ __attribute__((aligned(16))) u32x4 Xs[2][TT * 8];
+    __shared__ float colE[2][TC];
+    __shared__ __attribute__((aligned(16))) _Float16 colB[2][Q4 ? TC * 8 : 8];
+    __shared__ uint32_t last_flag;
 
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t wt = wave >> 1, wn = wave & 1;
-    // token tile fastest, so that token tile == XCD when ntok_tiles == 8
+    const uint32_t wt = wave >> 2, wn = wave & 3;
+    // token tile fastest, so that the XCDs (workgroup i runs on XCD i % 8) split by token tile
     const uint32_t tt = blockIdx.x % ntok_tiles, ct = blockIdx.x / ntok_tiles;
     const uint32_t t0 = tt * TT;
     constexpr uint32_t kRowsPerTile = PAIR ? TC / 2 : TC;
     const uint32_t r0 = ct * kRowsPerTile;
-    const uint32_t nb = cols / kQK, nsteps = cols / KS, ngroups = cols / 32;
+    const uint32_t nb = cols / kQK, ngroups = cols / 32;
+    const uint32_t kparts = gridDim.y, kp = blockIdx.y;
+    const uint32_t sb0 = kp * nb / kparts, sb1 = (kp + 1) * nb / kparts;
 
-    // producer role: column wc of the tile, k half hh
-    const uint32_t wc = tid >> 1, hh = tid & 1;
-    const uint8_t *wsrc = (PAIR && wc >= TC / 2) ? w1 : w0;
+    // producer role: column wc of the tile, k half hh (waves 0-3: hh 0, waves 4-7: hh 1)
+    const uint32_t wc = tid & (TC - 1), hh = tid / TC;
+    // PAIR: gate columns 0..127 come from waves with (wave & 3) < 2: wave-uniform
+    const rsrc_t wsrc = make_rsrc((PAIR && (wave & 3) >= 2) ? w1 : w0, wbytes);
     const uint32_t wrow = r0 + (PAIR ? (wc % (TC / 2)) : wc);
     const bool wvalid = wrow < rows;
+    const rsrc_t xsrc = make_rsrc(x, batch * cols * 2);
+    // x group sums: plane hi [batch][ngroups] then plane lo; rows past batch are
+    // never stored, so their (lo-plane) contents do not matter
+    const rsrc_t xssrc = make_rsrc(xsums, Q4 ? 2 * batch * ngroups * 2 : 0);
 
-    float16_t acc[2][2], tot[2][2];
+    float16_t acc[MI][NJ];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][j][v] = tot[i][j][v] = 0.f;
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
     auto bcol = [&](int j) -> uint32_t {
         if constexpr (PAIR) return uint32_t(j) * (TC / 2) + wn * 32;  // gate / up of the same 32 rows
-        else return wn * 64 + uint32_t(j) * 32;
+        else return wn * WC + uint32_t(j) * 32;
     };
+    // x(s) -> Xs[buf] by LDS DMA: instruction i of wave w fills rows 8*(w + 8i) .. +7;
+    // lane L writes LDS chunk L of that 1 KiB block, i.e. row +L/8, position L%8,
+    // so it fetches global chunk (L%8) ^ swizzle(row).  Rows past batch read 0.
+    auto dma_x = [&](uint32_t s, uint32_t buf) {
+#pragma unroll
+        for (int i = 0; i < XDMA; ++i) {
+            const uint32_t rbase = 8 * (wave + kWaves * uint32_t(i));
+            const uint32_t R = rbase + (lane >> 3), c = (lane & 7) ^ ((R >> 1) & 7);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                xsrc, (__attribute__((address_space(3))) void *)(&Xs[buf][rbase * 8]), 16,
+                ((t0 + R) * cols + s * KS + 8 * c) * 2, 0, 0, 0);
+        }
+    };
+    auto load_w = [&](uint32_t s, Raw<TYPE> &raw) { load_raw<LAYOUT>(wsrc, wrow, nb, s, hh, raw); };
 
-    for (uint32_t s = 0; s < nsteps; ++s) {
-        // ---- global -> registers
-        u32x4 xr[4];
+    Raw<TYPE> raw[2] = {};
+    u32x4 xsf[MI] = {};  // Q4_K: group sums of x for this super-block (hi in lanes 0-31, lo in 32-63)
+    const uint32_t sbeg = 4 * sb0;
+    load_w(sbeg, raw[0]);
+    dma_x(sbeg, 0);
+    load_w(sbeg + 1, raw[1]);
+
+    for (uint32_t sb = sb0; sb < sb1; ++sb) {
+        const uint32_t pb = (sb - sb0) & 1;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t idx = tid + kThreads * i, tok = idx >> 3, part = idx & 7;
-            const uint32_t t = t0 + tok;
-            xr[i] = t < batch ? *reinterpret_cast<const u32x4 *>(x + size_t(t) * cols + s * KS + part * 8)
-                              : u32x4{0u, 0u, 0u, 0u};
-        }
-        WRun wr;
-        u32x4 hdr = {0u, 0u, 0u, 0u};
-        uint32_t dbits = 0;
-        if (wvalid) {
-            if constexpr (TYPE == Q4_K) q4_tile<LAYOUT>(wsrc, wrow, nb, s, hh, wr, hdr);
-            else q6_tile<LAYOUT>(wsrc, wrow, nb, s, hh, wr, dbits);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) wr.v[i] = u32x4{0u, 0u, 0u, 0u};
-            wr.k_lo = TYPE == Q4_K ? 16 * int(hh) : 32 * int(hh);
-            wr.k_hi = TYPE == Q4_K ? 32 + 16 * int(hh) : 32 * int(hh) + 16;
-        }
-        __syncthreads();  // the previous step's fragments and column factors are consumed
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t idx = tid + kThreads * i, tok = idx >> 3, part = idx & 7;
-            *reinterpret_cast<u32x4 *>(&Xs[tok * LDSW + part * 8]) = xr[i];
-        }
-        {
-            _Float16 *wl = &Ws[wc * LDSW];
-            *reinterpret_cast<u32x4 *>(wl + wr.k_lo) = wr.v[0];
-            *reinterpret_cast<u32x4 *>(wl + wr.k_lo + 8) = wr.v[1];
-            *reinterpret_cast<u32x4 *>(wl + wr.k_hi) = wr.v[2];
-            *reinterpret_cast<u32x4 *>(wl + wr.k_hi + 8) = wr.v[3];
-        }
-        if ((s & 3) == 0 && hh == 0) {  // per-column factors of this super-block
-            if constexpr (TYPE == Q4_K) {
-                colD[wc] = lo_half(hdr.x);
-                colDmin[wc] = hi_half(hdr.x);
-                const Q4Scales sc = q4_scales(hdr.y, hdr.z, hdr.w);
-                u32x4 mv;
-#pragma unroll
-                for (int g = 0; g < 8; g += 2)
-                    mv[g / 2] = uint32_t(__builtin_bit_cast(uint16_t, _Float16(float(q4_m(sc, g))))) |
-                                (uint32_t(__builtin_bit_cast(uint16_t, _Float16(float(q4_m(sc, g + 1))))) << 16);
-                *reinterpret_cast<u32x4 *>(&colM[wc * 8]) = mv;
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t s = 4 * sb + uint32_t(j), buf = uint32_t(j) & 1;
+            Raw<TYPE> &rw = raw[j & 1];
+            // ---- per-row factors and the weight tile of step s
+            float d, e;
+            if constexpr (Q4) {
+                d = lo_half(rw.hdr.x);
+                const float dmin = hi_half(rw.hdr.x);
+                e = __builtin_fmaxf(d, dmin * 0.0009765625f);
+                e = e > 0.f ? e : 1.f;
             } else {
-                colD[wc] = lo_half(dbits);
+                d = lo_half(rw.dbits);
+                e = d != 0.f ? d : 1.f;
             }
-        }
-        __syncthreads();
-
-        // ---- MFMA over the 4 k16 sub-steps
-#pragma unroll
-        for (int kk = 0; kk < KS / 16; ++kk) {
-            const uint32_t koff = 16 * kk + 8 * (lane >> 5);
-            half8_t a[2], b[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-                a[i] = *reinterpret_cast<const half8_t *>(&Xs[(wt * 64 + i * 32 + (lane & 31)) * LDSW + koff]);
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                b[j] = *reinterpret_cast<const half8_t *>(&Ws[(bcol(j) + (lane & 31)) * LDSW + koff]);
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
-        }
-
-        if ((s & 3) == 3) {  // end of a super-block: apply the per-row factors
-            const uint32_t sb = s >> 2;
-            float dcol[2];
-#pragma unroll
-            for (int j = 0; j < 2; ++j) dcol[j] = colD[bcol(j) + (lane & 31)];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) {
-                        tot[i][j][v] = __builtin_fmaf(dcol[j], acc[i][j][v], tot[i][j][v]);
-                        acc[i][j][v] = 0.f;
-                    }
-            if constexpr (TYPE == Q4_K) {
-                // min term: A = group sums of x (hi in k 0..7, lo in k 8..15), B = m_g
-                half8_t am[2], bm[2];
-#pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    const uint32_t t = t0 + wt * 64 + i * 32 + (lane & 31);
-                    const uint16_t *src = (lane < 32 ? xs_hi : xs_lo) + size_t(t) * ngroups + 8 * sb;
-                    am[i] = t < batch ? *reinterpret_cast<const half8_t *>(src) : half8_t{};
-                }
-                float dmin[2];
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const uint32_t c = bcol(j) + (lane & 31);
-                    bm[j] = *reinterpret_cast<const half8_t *>(&colM[c * 8]);
-                    dmin[j] = colDmin[c];
-                }
-#pragma unroll
-                for (int i = 0; i < 2; ++i)
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        const float16_t mt = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[i], bm[j], float16_t{}, 0, 0, 0);
-#pragma unroll
-                        for (int v = 0; v < 16; ++v) tot[i][j][v] = __builtin_fmaf(-dmin[j], mt[v], tot[i][j][v]);
-                    }
+            WRun wr;
+            decode(rw, s, hh, d / e, wr);
+            {
+                _Float16 *wl = &Ws[buf][wc * LDSW];
+                *reinterpret_cast<u32x4 *>(wl + k_lo(TYPE, hh)) = wr.v[0];
+                *reinterpret_cast<u32x4 *>(wl + k_lo(TYPE, hh) + 8) = wr.v[1];
+                *reinterpret_cast<u32x4 *>(wl + k_hi(TYPE, hh)) = wr.v[2];
+                *reinterpret_cast<u32x4 *>(wl + k_hi(TYPE, hh) + 8) = wr.v[3];
             }
-            if constexpr (ACC == ACC_FP16) {
+            if (j == 0 && hh == 0) {
+                colE[pb][wc] = e;
+                if constexpr (Q4) {
+                    const float f = -hi_half(rw.hdr.x) / e;
+                    const Q4Scales sc = q4_scales(rw.hdr.y, rw.hdr.z, rw.hdr.w);
+                    u32x4 mv;
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
+                    for (int g = 0; g < 8; g += 2)
+                        mv[g / 2] = uint32_t(__builtin_bit_cast(uint16_t, _Float16(f * float(q4_m(sc, g))))) |
+                                    (uint32_t(__builtin_bit_cast(uint16_t, _Float16(f * float(q4_m(sc, g + 1))))) << 16);
+                    *reinterpret_cast<u32x4 *>(&colB[pb][wc * 8]) = mv;
+                }
+            }
+            // ---- the x DMA of step s was issued before raw(s+1): wait for it, not for raw(s+1)
+            __builtin_amdgcn_s_waitcnt(int((kRawLoads & 15) | ((kRawLoads >> 4) << 14) | (7 << 4) | (15 << 8)));
+            __syncthreads();
+            // ---- refill: x(s+1) -> Xs[buf ^ 1], raw(s+2) -> the slot just decoded
+            if constexpr (Q4) {
+                if (j == 0) {
 #pragma unroll
-                    for (int j = 0; j < 2; ++j)
+                    for (int i = 0; i < MI; ++i)
+                        xsf[i] = bload16(xssrc, ((lane >> 5) * batch * ngroups +
+                                                 (t0 + wt * WT + i * 32 + (lane & 31)) * ngroups + 8 * sb) * 2);
+                }
+            }
+            dma_x(s + 1, buf ^ 1);
+            load_w(s + 2, rw);
+
+            if (j == 0 && sb > sb0) {  // enter super-block sb: S/e_prev -> S/e_sb
 #pragma unroll
-                        for (int v = 0; v < 16; ++v) tot[i][j][v] = round_f16p(tot[i][j][v]);
+                for (int jj = 0; jj < NJ; ++jj) {
+                    const uint32_t c = bcol(jj) + (lane & 31);
+                    const float e_prev = colE[pb ^ 1][c], e_cur = colE[pb][c];
+                    const float r = e_prev / e_cur, rinv = 1.0f / e_cur;
+#pragma unroll
+                    for (int i = 0; i < MI; ++i)
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) {
+                            if constexpr (ACC == ACC_FP16) acc[i][jj][v] = round_f16p(acc[i][jj][v] * e_prev) * rinv;
+                            else acc[i][jj][v] *= r;
+                        }
+                }
+            }
+
+            // ---- MFMA over the 4 k16 sub-steps
+#pragma unroll
+            for (int kk = 0; kk < KS / 16; ++kk) {
+                const uint32_t koff = 16 * kk + 8 * (lane >> 5);
+                half8_t a[MI], b[NJ];
+#pragma unroll
+                for (int jj = 0; jj < NJ; ++jj)
+                    b[jj] = *reinterpret_cast<const half8_t *>(&Ws[buf][(bcol(jj) + (lane & 31)) * LDSW + koff]);
+#pragma unroll
+                for (int i = 0; i < MI; ++i) {
+                    const uint32_t R = wt * WT + i * 32 + (lane & 31);
+                    const uint32_t c = 2 * kk + (lane >> 5);
+                    a[i] = __builtin_bit_cast(half8_t, Xs[buf][R * 8 + (c ^ ((R >> 1) & 7))]);
+                }
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int jj = 0; jj < NJ; ++jj)
+                        acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[jj], acc[i][jj], 0, 0, 0);
+            }
+
+            if constexpr (Q4) {
+                if (j == 3) {  // min term of super-block sb
+#pragma unroll
+                    for (int jj = 0; jj < NJ; ++jj) {
+                        const half8_t bm = *reinterpret_cast<const half8_t *>(&colB[pb][(bcol(jj) + (lane & 31)) * 8]);
+#pragma unroll
+                        for (int i = 0; i < MI; ++i)
+                            acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, xsf[i]), bm,
+                                                                                acc[i][jj], 0, 0, 0);
+                    }
+                }
             }
         }
     }
 
-    // ---- epilogue.  32x32 D layout: lane holds column lane%32 and rows
-    // 8*(v/4) + 4*(lane/32) + v%4 for v = 0..15.
+    // ---- S = acc * e_last.  32x32 D layout: lane holds column lane%32 and
+    // rows 8*(v/4) + 4*(lane/32) + v%4 for v = 0..15.
+    const uint32_t pl = (sb1 - 1 - sb0) & 1;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int jj = 0; jj < NJ; ++jj) {
+        const float el = colE[pl][bcol(jj) + (lane & 31)];
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                acc[i][jj][v] *= el;
+                if constexpr (ACC == ACC_FP16) acc[i][jj][v] = round_f16p(acc[i][jj][v]);
+            }
+    }
+    auto tok_of = [&](int i, int v) -> uint32_t {
+        return t0 + wt * WT + uint32_t(i) * 32 + 8 * uint32_t(v >> 2) + 4 * (lane >> 5) + uint32_t(v & 3);
+    };
+    auto col_row = [&](int jj) -> uint32_t {  // weight row of B fragment jj
+        if constexpr (PAIR) return r0 + wn * 32 + (lane & 31);
+        else return r0 + bcol(jj) + (lane & 31);
+    };
+
+    if (kparts > 1) {
+        // partial layout [kp][jj-plane (PAIR: gate, up)][batch][rows]
+        constexpr uint32_t kPlanes = PAIR ? 2 : 1;
+        auto pidx = [&](uint32_t part, int jj, uint32_t t, uint32_t r) -> size_t {
+            return ((size_t(part) * kPlanes + (PAIR ? uint32_t(jj) : 0u)) * batch + t) * rows + r;
+        };
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const uint32_t t = tok_of(i, v);
+#pragma unroll
+                for (int jj = 0; jj < NJ; ++jj) {
+                    const uint32_t r = col_row(jj);
+                    if (t < batch && r < rows)
+                        __hip_atomic_store(&partial[pidx(kp, jj, t, r)], acc[i][jj][v], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __syncthreads();  // every wave's parts are stored
+        if (tid == 0) {
+            const uint32_t prev =
+                __hip_atomic_fetch_add(&counters[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last_flag = prev == kparts - 1;
+        }
+        __syncthreads();
+        if (!last_flag) return;
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const uint32_t t = tok_of(i, v);
+#pragma unroll
+                for (int jj = 0; jj < NJ; ++jj) {
+                    const uint32_t r = col_row(jj);
+                    float sum = 0.f;
+                    if (t < batch && r < rows)
+                        for (uint32_t part = 0; part < kparts; ++part)
+                            sum += __hip_atomic_load(&partial[pidx(part, jj, t, r)], __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+                    acc[i][jj][v] = ACC == ACC_FP16 ? round_f16p(sum) : sum;
+                }
+            }
+        if (tid == 0) __hip_atomic_store(&counters[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-            const uint32_t t = t0 + wt * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+            const uint32_t t = tok_of(i, v);
             if (t >= batch) continue;
             if constexpr (PAIR) {
-                const uint32_t r = r0 + wn * 32 + (lane & 31);
-                const float g = tot[i][0][v], u = tot[i][1][v];
-                reinterpret_cast<_Float16 *>(out)[size_t(t) * rows + r] = _Float16(gelu_tanh(g) * u);
+                const uint32_t r = col_row(0);
+                if (r < rows)
+                    reinterpret_cast<_Float16 *>(out)[size_t(t) * rows + r] =
+                        _Float16(gelu_tanh(acc[i][0][v]) * acc[i][1][v]);
             } else {
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const uint32_t r = r0 + wn * 64 + j * 32 + (lane & 31);
-                    if (r < rows) reinterpret_cast<float *>(out)[size_t(t) * rows + r] = tot[i][j][v];
+                for (int jj = 0; jj < NJ; ++jj) {
+                    const uint32_t r = col_row(jj);
+                    if (r < rows) reinterpret_cast<float *>(out)[size_t(t) * rows + r] = acc[i][jj][v];
                 }
             }
         }
@@ -376,36 +533,67 @@ __global__ void group_sums_kernel(const uint16_t *__restrict__ x, uint32_t cols,
     lo[idx] = __builtin_bit_cast(uint16_t, _Float16(s - float(h)));
 }
 
+struct GemmPlan {
+    uint32_t ntok, ncol, kparts;
+};
+
+// Output tiles and split of K: enough workgroups to cover most of the 256 CUs
+// (the 3840-row down projection has only 4 x 15 tiles at batch 1024).
+GemmPlan plan_gemm(uint32_t cols, uint32_t rows, uint32_t batch, bool pair) {
+    GemmPlan p;
+    p.ntok = (batch + TT - 1) / TT;
+    const uint32_t rows_per_tile = pair ? TC / 2 : TC;
+    p.ncol = (rows + rows_per_tile - 1) / rows_per_tile;
+    const uint32_t nb = cols / kQK, tiles = p.ntok * p.ncol;
+    p.kparts = 1;
+    while (tiles * p.kparts < 200 && p.kparts * 2 <= nb / 4) p.kparts *= 2;
+    if (const char *e = getenv("NS_GEMM_KPARTS"); e && *e) {
+        const int v = atoi(e);
+        if (v >= 1 && uint32_t(v) <= nb) p.kparts = uint32_t(v);
+    }
+    return p;
+}
+
 template <int TYPE, int LAYOUT, bool PAIR>
 hipError_t launch_mode(int acc, const uint8_t *w, const uint8_t *up, const uint16_t *x, const uint16_t *xh,
-                       const uint16_t *xl, void *out, uint32_t cols, uint32_t rows, uint32_t batch,
-                       hipStream_t stream) {
-    const uint32_t ntok = (batch + TT - 1) / TT;
-    const uint32_t rows_per_tile = PAIR ? TC / 2 : TC;
-    const uint32_t ncol = (rows + rows_per_tile - 1) / rows_per_tile;
-    const dim3 grid(ntok * ncol), block(kThreads);
+                       void *out, uint32_t cols, uint32_t rows, uint32_t batch, const Workspace &ws,
+                       size_t ws_offset, hipStream_t stream) {
+    const GemmPlan p = plan_gemm(cols, rows, batch, PAIR);
+    const dim3 grid(p.ntok * p.ncol, p.kparts), block(kThreads);
+    const uint32_t wbytes = rows * (cols / kQK) * block_bytes(TYPE);
+    float *partial = ws.partial + ws_offset;
     if (acc == ACC_FP16)
-        gemm_kernel<TYPE, LAYOUT, ACC_FP16, PAIR><<<grid, block, 0, stream>>>(w, up, x, xh, xl, out, cols, rows,
-                                                                              batch, ntok);
+        gemm_kernel<TYPE, LAYOUT, ACC_FP16, PAIR><<<grid, block, 0, stream>>>(
+            w, up, x, xh, out, partial, ws.counters, cols, rows, batch, p.ntok, wbytes);
     else
-        gemm_kernel<TYPE, LAYOUT, ACC_FP32, PAIR><<<grid, block, 0, stream>>>(w, up, x, xh, xl, out, cols, rows,
-                                                                              batch, ntok);
+        gemm_kernel<TYPE, LAYOUT, ACC_FP32, PAIR><<<grid, block, 0, stream>>>(
+            w, up, x, xh, out, partial, ws.counters, cols, rows, batch, p.ntok, wbytes);
     return hipGetLastError();
 }
 
 template <int TYPE, bool PAIR>
 hipError_t launch_layout(int layout, int acc, const uint8_t *w, const uint8_t *up, const uint16_t *x,
-                         const uint16_t *xh, const uint16_t *xl, void *out, uint32_t cols, uint32_t rows,
-                         uint32_t batch, hipStream_t stream) {
-    if (layout == CDNA4) return launch_mode<TYPE, CDNA4, PAIR>(acc, w, up, x, xh, xl, out, cols, rows, batch, stream);
-    return launch_mode<TYPE, NSMFFN, PAIR>(acc, w, up, x, xh, xl, out, cols, rows, batch, stream);
+                         const uint16_t *xh, void *out, uint32_t cols, uint32_t rows, uint32_t batch,
+                         const Workspace &ws, size_t ws_offset, hipStream_t stream) {
+    if (layout == CDNA4)
+        return launch_mode<TYPE, CDNA4, PAIR>(acc, w, up, x, xh, out, cols, rows, batch, ws, ws_offset, stream);
+    return launch_mode<TYPE, NSMFFN, PAIR>(acc, w, up, x, xh, out, cols, rows, batch, ws, ws_offset, stream);
 }
 
 }  // namespace
 
-size_t gemm_workspace_floats(int type, uint32_t cols, uint32_t batch) {
-    // two fp16 planes of batch x cols/32 group sums, counted in floats
-    return type == Q4_K ? (size_t(batch) * (cols / 32) + 1) : 0;
+// Workspace layout: [Q4_K group sums of x: 2 fp16 planes of batch x cols/32,
+// counted in floats and rounded up to 64] [split-K parts: kparts x planes x batch x rows].
+static size_t xs_floats(int type, uint32_t cols, uint32_t batch) {
+    return type == Q4_K ? ((size_t(batch) * (cols / 32) + 63) / 64) * 64 : 0;
+}
+
+void gemm_workspace_need(int type, uint32_t cols, uint32_t rows, uint32_t batch, bool pair, size_t *floats,
+                         size_t *counters) {
+    const GemmPlan p = plan_gemm(cols, rows, batch, pair);
+    *floats = xs_floats(type, cols, batch) +
+              (p.kparts > 1 ? size_t(p.kparts) * (pair ? 2 : 1) * batch * rows : 0);
+    *counters = size_t(p.ntok) * p.ncol;
 }
 
 hipError_t launch_gemm(int type, int layout, int acc, const uint8_t *w, const uint8_t *up, const uint16_t *x,
@@ -419,9 +607,11 @@ hipError_t launch_gemm(int type, int layout, int acc, const uint8_t *w, const ui
         group_sums_kernel<<<dim3(uint32_t((n + 255) / 256)), dim3(256), 0, stream>>>(x, cols, batch, xh, xl);
         if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     }
-    if (up) return launch_layout<Q4_K, true>(layout, acc, w, up, x, xh, xl, out, cols, rows, batch, stream);
-    if (type == Q4_K) return launch_layout<Q4_K, false>(layout, acc, w, nullptr, x, xh, xl, out, cols, rows, batch, stream);
-    return launch_layout<Q6_K, false>(layout, acc, w, nullptr, x, xh, xl, out, cols, rows, batch, stream);
+    const size_t off = xs_floats(type, cols, batch);
+    if (up) return launch_layout<Q4_K, true>(layout, acc, w, up, x, xh, out, cols, rows, batch, ws, off, stream);
+    if (type == Q4_K)
+        return launch_layout<Q4_K, false>(layout, acc, w, nullptr, x, xh, out, cols, rows, batch, ws, off, stream);
+    return launch_layout<Q6_K, false>(layout, acc, w, nullptr, x, xh, out, cols, rows, batch, ws, off, stream);
 }
 
 }  // namespace ns

@@ -32,8 +32,9 @@ hipError_t launch_gemv(int type, int layout, const uint8_t *w, const uint8_t *up
 void gemv_workspace_need(uint32_t cols, uint32_t rows, bool pair, size_t *partial_floats,
                          size_t *counters);
 
-// Workspace (in floats) the prefill GEMM needs: Q4_K keeps fp16 hi/lo group sums of x.
-size_t gemm_workspace_floats(int type, uint32_t cols, uint32_t batch);
+// Workspace the prefill GEMM needs: Q4_K group sums of x, split-K parts, tile counters.
+void gemm_workspace_need(int type, uint32_t cols, uint32_t rows, uint32_t batch, bool pair, size_t *floats,
+                         size_t *counters);
 
 // Prefill GEMM over fp16 x [batch][cols]: plain (fp32 out [batch][rows]) or the
 // gate/up pair with GeGLU (fp16 h [batch][rows]).
