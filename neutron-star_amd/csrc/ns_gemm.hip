@@ -247,7 +247,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, const uint16_t *__restrict__ x,
     const uint16_t *__restrict__ xsums, void *__restrict__ out, float *__restrict__ partial,
     uint32_t *__restrict__ counters, uint32_t cols, uint32_t rows, uint32_t batch, uint32_t ntok_tiles,
-    uint32_t wbytes) {
+    uint32_t ncol_tiles, uint32_t kparts_total, uint32_t wbytes) {
     constexpr bool Q4 = TYPE == Q4_K;
     constexpr uint32_t kRawLoads = Q4 ? 2 : (LAYOUT == CDNA4 ? 6 : 41);  // vector loads per load_raw
     __shared__ __attribute__((aligned(16))) _Float16 Ws[2][TC * LDSW];
@@ -259,13 +259,20 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wt = wave >> 2, wn = wave & 3;
-    // token tile fastest, so that the XCDs (workgroup i runs on XCD i % 8) split by token tile
-    const uint32_t tt = blockIdx.x % ntok_tiles, ct = blockIdx.x / ntok_tiles;
+    // XCD-aware order.  Workgroup L is dispatched to XCD L % 8; the work items are
+    // numbered q = (kp * ntok + tt) * ncol + ct (one x slice = fixed (tt, kp) and
+    // all its column tiles) and XCD x takes the contiguous run q in
+    // [x * W/8, (x+1) * W/8), so each XCD's L2 holds whole x slices and the
+    // column tiles that share one are resident together.
+    const uint32_t nwg = gridDim.x, w8 = nwg / 8, L = blockIdx.x;
+    const uint32_t q = L < 8 * w8 ? (L % 8) * w8 + L / 8 : L;
+    const uint32_t ncol = ncol_tiles, kparts = kparts_total;
+    const uint32_t ct = q % ncol, g = q / ncol, tt = g % ntok_tiles, kp = g / ntok_tiles;
+    const uint32_t tile = tt + ntok_tiles * ct;  // counter slot of the output tile
     const uint32_t t0 = tt * TT;
     constexpr uint32_t kRowsPerTile = PAIR ? TC / 2 : TC;
     const uint32_t r0 = ct * kRowsPerTile;
     const uint32_t nb = cols / kQK, ngroups = cols / 32;
-    const uint32_t kparts = gridDim.y, kp = blockIdx.y;
     const uint32_t sb0 = kp * nb / kparts, sb1 = (kp + 1) * nb / kparts;
 
     // producer role: column wc of the tile, k half hh (waves 0-3: hh 0, waves 4-7: hh 1)
@@ -308,54 +315,68 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
 
     Raw<TYPE> raw[2] = {};
     u32x4 xsf[MI] = {};  // Q4_K: group sums of x for this super-block (hi in lanes 0-31, lo in 32-63)
+
+    // Decode raw weights of step s into weight buffer s&1 (and, on the first step
+    // of a super-block, its per-row factors).
+    auto produce = [&](uint32_t s, const Raw<TYPE> &rw) {
+        const uint32_t buf = s & 1, pb = ((s >> 2) - sb0) & 1;
+        float d, e;
+        if constexpr (Q4) {
+            d = lo_half(rw.hdr.x);
+            e = __builtin_fmaxf(d, hi_half(rw.hdr.x) * 0.0009765625f);
+            e = e > 0.f ? e : 1.f;
+        } else {
+            d = lo_half(rw.dbits);
+            e = d != 0.f ? d : 1.f;
+        }
+        const float re = __builtin_amdgcn_rcpf(e);  // ~1 ulp; exactness is kept by z = 1 when e == d
+        const float z = d == e ? 1.f : d * re;
+        WRun wr;
+        decode(rw, s, hh, z, wr);
+        _Float16 *wl = &Ws[buf][wc * LDSW];
+        *reinterpret_cast<u32x4 *>(wl + k_lo(TYPE, hh)) = wr.v[0];
+        *reinterpret_cast<u32x4 *>(wl + k_lo(TYPE, hh) + 8) = wr.v[1];
+        *reinterpret_cast<u32x4 *>(wl + k_hi(TYPE, hh)) = wr.v[2];
+        *reinterpret_cast<u32x4 *>(wl + k_hi(TYPE, hh) + 8) = wr.v[3];
+        if ((s & 3) == 0 && hh == 0) {
+            colE[pb][wc] = e;
+            if constexpr (Q4) {
+                const float f = -hi_half(rw.hdr.x) * re;
+                const Q4Scales sc = q4_scales(rw.hdr.y, rw.hdr.z, rw.hdr.w);
+                u32x4 mv;
+#pragma unroll
+                for (int g = 0; g < 8; g += 2)
+                    mv[g / 2] = uint32_t(__builtin_bit_cast(uint16_t, _Float16(f * float(q4_m(sc, g))))) |
+                                (uint32_t(__builtin_bit_cast(uint16_t, _Float16(f * float(q4_m(sc, g + 1))))) << 16);
+                *reinterpret_cast<u32x4 *>(&colB[pb][wc * 8]) = mv;
+            }
+        }
+    };
+    // The x DMA of the next step is issued before the next raw loads: wait for
+    // it but let those raw loads stay in flight.
+    auto wait_x = [&]() {
+        __builtin_amdgcn_s_waitcnt(int((kRawLoads & 15) | ((kRawLoads >> 4) << 14) | (7 << 4) | (15 << 8)));
+    };
+
+    // prologue: step sbeg ready in LDS, raw(sbeg+1) in flight
     const uint32_t sbeg = 4 * sb0;
     load_w(sbeg, raw[0]);
     dma_x(sbeg, 0);
     load_w(sbeg + 1, raw[1]);
+    produce(sbeg, raw[0]);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
 
+    // Step s: issue x(s+1) -> Xs[buf^1] and raw(s+2); MFMAs of s on buffers buf,
+    // with the decode of raw(s+1) into Ws[buf^1] placed among them so the VALU
+    // work runs in the MFMA shadow; then wait for x(s+1) and meet at the barrier.
+    // Buffers buf^1 were last read by MFMAs of step s-1, finished before barrier s.
     for (uint32_t sb = sb0; sb < sb1; ++sb) {
         const uint32_t pb = (sb - sb0) & 1;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const uint32_t s = 4 * sb + uint32_t(j), buf = uint32_t(j) & 1;
-            Raw<TYPE> &rw = raw[j & 1];
-            // ---- per-row factors and the weight tile of step s
-            float d, e;
-            if constexpr (Q4) {
-                d = lo_half(rw.hdr.x);
-                const float dmin = hi_half(rw.hdr.x);
-                e = __builtin_fmaxf(d, dmin * 0.0009765625f);
-                e = e > 0.f ? e : 1.f;
-            } else {
-                d = lo_half(rw.dbits);
-                e = d != 0.f ? d : 1.f;
-            }
-            WRun wr;
-            decode(rw, s, hh, d / e, wr);
-            {
-                _Float16 *wl = &Ws[buf][wc * LDSW];
-                *reinterpret_cast<u32x4 *>(wl + k_lo(TYPE, hh)) = wr.v[0];
-                *reinterpret_cast<u32x4 *>(wl + k_lo(TYPE, hh) + 8) = wr.v[1];
-                *reinterpret_cast<u32x4 *>(wl + k_hi(TYPE, hh)) = wr.v[2];
-                *reinterpret_cast<u32x4 *>(wl + k_hi(TYPE, hh) + 8) = wr.v[3];
-            }
-            if (j == 0 && hh == 0) {
-                colE[pb][wc] = e;
-                if constexpr (Q4) {
-                    const float f = -hi_half(rw.hdr.x) / e;
-                    const Q4Scales sc = q4_scales(rw.hdr.y, rw.hdr.z, rw.hdr.w);
-                    u32x4 mv;
-#pragma unroll
-                    for (int g = 0; g < 8; g += 2)
-                        mv[g / 2] = uint32_t(__builtin_bit_cast(uint16_t, _Float16(f * float(q4_m(sc, g))))) |
-                                    (uint32_t(__builtin_bit_cast(uint16_t, _Float16(f * float(q4_m(sc, g + 1))))) << 16);
-                    *reinterpret_cast<u32x4 *>(&colB[pb][wc * 8]) = mv;
-                }
-            }
-            // ---- the x DMA of step s was issued before raw(s+1): wait for it, not for raw(s+1)
-            __builtin_amdgcn_s_waitcnt(int((kRawLoads & 15) | ((kRawLoads >> 4) << 14) | (7 << 4) | (15 << 8)));
-            __syncthreads();
-            // ---- refill: x(s+1) -> Xs[buf ^ 1], raw(s+2) -> the slot just decoded
+            const bool more = s + 1 < 4 * sb1;
             if constexpr (Q4) {
                 if (j == 0) {
 #pragma unroll
@@ -364,15 +385,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
                                                  (t0 + wt * WT + i * 32 + (lane & 31)) * ngroups + 8 * sb) * 2);
                 }
             }
-            dma_x(s + 1, buf ^ 1);
-            load_w(s + 2, rw);
+            if (more) dma_x(s + 1, buf ^ 1);
+            load_w(s + 2, raw[j & 1]);  // slot of raw(s), decoded during step s-1
 
             if (j == 0 && sb > sb0) {  // enter super-block sb: S/e_prev -> S/e_sb
 #pragma unroll
                 for (int jj = 0; jj < NJ; ++jj) {
                     const uint32_t c = bcol(jj) + (lane & 31);
                     const float e_prev = colE[pb ^ 1][c], e_cur = colE[pb][c];
-                    const float r = e_prev / e_cur, rinv = 1.0f / e_cur;
+                    const float rinv = __builtin_amdgcn_rcpf(e_cur), r = e_prev * rinv;
 #pragma unroll
                     for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -383,25 +404,31 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
                 }
             }
 
-            // ---- MFMA over the 4 k16 sub-steps
-#pragma unroll
-            for (int kk = 0; kk < KS / 16; ++kk) {
+            // ---- MFMAs of step s over 4 k16 sub-steps, decode of step s+1 in between.
+            // Fragments of sub-step kk+1 are read from LDS while kk's MFMAs run.
+            half8_t a[2][MI], b[2][NJ];
+            auto frags = [&](int kk, half8_t (&fa)[MI], half8_t (&fb)[NJ]) {
                 const uint32_t koff = 16 * kk + 8 * (lane >> 5);
-                half8_t a[MI], b[NJ];
 #pragma unroll
                 for (int jj = 0; jj < NJ; ++jj)
-                    b[jj] = *reinterpret_cast<const half8_t *>(&Ws[buf][(bcol(jj) + (lane & 31)) * LDSW + koff]);
+                    fb[jj] = *reinterpret_cast<const half8_t *>(&Ws[buf][(bcol(jj) + (lane & 31)) * LDSW + koff]);
 #pragma unroll
                 for (int i = 0; i < MI; ++i) {
                     const uint32_t R = wt * WT + i * 32 + (lane & 31);
                     const uint32_t c = 2 * kk + (lane >> 5);
-                    a[i] = __builtin_bit_cast(half8_t, Xs[buf][R * 8 + (c ^ ((R >> 1) & 7))]);
+                    fa[i] = __builtin_bit_cast(half8_t, Xs[buf][R * 8 + (c ^ ((R >> 1) & 7))]);
                 }
+            };
+            frags(0, a[0], b[0]);
+#pragma unroll
+            for (int kk = 0; kk < KS / 16; ++kk) {
+                if (kk + 1 < KS / 16) frags(kk + 1, a[(kk + 1) & 1], b[(kk + 1) & 1]);
 #pragma unroll
                 for (int i = 0; i < MI; ++i)
 #pragma unroll
                     for (int jj = 0; jj < NJ; ++jj)
-                        acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[jj], acc[i][jj], 0, 0, 0);
+                        acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kk & 1][i], b[kk & 1][jj], acc[i][jj], 0, 0, 0);
+                if (kk == 1 && more) produce(s + 1, raw[(j + 1) & 1]);
             }
 
             if constexpr (Q4) {
@@ -416,6 +443,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
                     }
                 }
             }
+            wait_x();
+            __syncthreads();
         }
     }
 
@@ -466,7 +495,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
         __syncthreads();  // every wave's parts are stored
         if (tid == 0) {
             const uint32_t prev =
-                __hip_atomic_fetch_add(&counters[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             last_flag = prev == kparts - 1;
         }
         __syncthreads();
@@ -487,7 +516,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
                     acc[i][jj][v] = ACC == ACC_FP16 ? round_f16p(sum) : sum;
                 }
             }
-        if (tid == 0) __hip_atomic_store(&counters[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
 #pragma unroll
@@ -559,15 +588,15 @@ hipError_t launch_mode(int acc, const uint8_t *w, const uint8_t *up, const uint1
                        void *out, uint32_t cols, uint32_t rows, uint32_t batch, const Workspace &ws,
                        size_t ws_offset, hipStream_t stream) {
     const GemmPlan p = plan_gemm(cols, rows, batch, PAIR);
-    const dim3 grid(p.ntok * p.ncol, p.kparts), block(kThreads);
+    const dim3 grid(p.ntok * p.ncol * p.kparts), block(kThreads);
     const uint32_t wbytes = rows * (cols / kQK) * block_bytes(TYPE);
     float *partial = ws.partial + ws_offset;
     if (acc == ACC_FP16)
         gemm_kernel<TYPE, LAYOUT, ACC_FP16, PAIR><<<grid, block, 0, stream>>>(
-            w, up, x, xh, out, partial, ws.counters, cols, rows, batch, p.ntok, wbytes);
+            w, up, x, xh, out, partial, ws.counters, cols, rows, batch, p.ntok, p.ncol, p.kparts, wbytes);
     else
         gemm_kernel<TYPE, LAYOUT, ACC_FP32, PAIR><<<grid, block, 0, stream>>>(
-            w, up, x, xh, out, partial, ws.counters, cols, rows, batch, p.ntok, wbytes);
+            w, up, x, xh, out, partial, ws.counters, cols, rows, batch, p.ntok, p.ncol, p.kparts, wbytes);
     return hipGetLastError();
 }
 
