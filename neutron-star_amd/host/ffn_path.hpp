@@ -1,0 +1,152 @@
+// ffn_path.hpp -- C++ host layer over the C ABI (include/ns_ffn.h) that keeps
+// the reference engine's FFN call surface (src/native/metal_engine.mm):
+//
+//   matmul(e, w, in, out, batch, half_input)          mm:269-275
+//   gate_up_geglu_rm32(e, gate, up, in, out, batch, fast_swa)   mm:288
+//   gate_up_geglu_decode(e, gate, up, in, out)        mm:290
+//   ffn_down(e, w, in, out, batch, half_input, fast_swa)        mm:289
+//
+// The reference passes an id<MTLComputeCommandEncoder>; here the first
+// argument is the hipStream_t the work is ordered on.  Weights are addressed
+// the way the reference addresses them: one device image of the weight file
+// plus a per-tensor byte offset and layout (MetalFfnFile::offset / reordered,
+// src/native/metal_ffn.cpp:300-311).  Failures throw std::runtime_error with
+// the C ABI's message, the reference's error convention (mm:231-243).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+#include <utility>
+#include <vector>
+
+#include "ns_ffn.h"
+
+namespace neutron::amd {
+
+// GGUF tensor types used on this path (include/neutron/native/gguf.hpp:13).
+enum class TensorType : uint32_t { F32 = 0, F16 = 1, Q4_K = 12, Q6_K = 14 };
+
+// Descriptor of one weight tensor, as in gguf.hpp:20-27: shape[0] = cols (K),
+// shape[1] = rows (N); `offset` identifies the tensor (the GGUF data offset).
+struct Tensor {
+    std::string name;
+    std::vector<uint64_t> shape;
+    TensorType type{};
+    uint64_t offset = 0;
+    uint64_t bytes = 0;
+};
+
+enum class Layout : int { RowMajor = NS_LAYOUT_ROW_MAJOR, Nsmffn = NS_LAYOUT_NSMFFN, Cdna4 = NS_LAYOUT_CDNA4 };
+
+inline void check(int rc) {
+    if (rc != NS_OK) throw std::runtime_error(std::string("neutron-star-amd: ") + ns_last_error());
+}
+
+// A device image of the weights: one allocation, each tensor at a byte offset
+// in a given layout (the role MetalFfnFile plays for the Metal engine).
+class WeightImage {
+public:
+    WeightImage() = default;
+    WeightImage(const WeightImage &) = delete;
+    WeightImage &operator=(const WeightImage &) = delete;
+    ~WeightImage() {
+        if (base_) (void)hipFree(base_);
+    }
+
+    // Allocate `bytes` of device memory for the image.
+    void allocate(size_t bytes) {
+        if (base_) throw std::runtime_error("weight image already allocated");
+        if (hipMalloc(&base_, bytes) != hipSuccess) throw std::runtime_error("weight image allocation failed");
+        size_ = bytes;
+    }
+    // Copy host bytes of one tensor into the image at `image_offset` and
+    // register it; with `retile_to_cdna4`, NSMFFN / ROW_MAJOR input is converted
+    // on the device into the CDNA4 layout (the conversion step at load time).
+    void upload(const Tensor &t, const void *host, uint64_t image_offset, Layout layout, bool retile_to_cdna4,
+                hipStream_t stream) {
+        if (!base_ || image_offset + t.bytes > size_) throw std::runtime_error("tensor outside the weight image: " + t.name);
+        uint8_t *dst = static_cast<uint8_t *>(base_) + image_offset;
+        if (!retile_to_cdna4 || layout == Layout::Cdna4 || t.type == TensorType::F32 || t.type == TensorType::F16) {
+            if (hipMemcpyAsync(dst, host, t.bytes, hipMemcpyHostToDevice, stream) != hipSuccess)
+                throw std::runtime_error("weight upload failed: " + t.name);
+            entries_[t.offset] = {image_offset, layout};
+            return;
+        }
+        void *tmp = nullptr;
+        if (hipMalloc(&tmp, t.bytes) != hipSuccess) throw std::runtime_error("staging allocation failed");
+        bool ok = hipMemcpyAsync(tmp, host, t.bytes, hipMemcpyHostToDevice, stream) == hipSuccess;
+        int rc = ok ? ns_retile_device(tmp, dst, int(t.type), uint32_t(t.shape.at(0)), uint32_t(t.shape.at(1)),
+                                       int(layout), NS_LAYOUT_CDNA4, stream)
+                    : NS_ERR_HIP;
+        ok = ok && rc == NS_OK && hipStreamSynchronize(stream) == hipSuccess;
+        (void)hipFree(tmp);
+        if (!ok) throw std::runtime_error("weight conversion failed: " + t.name + ": " + ns_last_error());
+        entries_[t.offset] = {image_offset, Layout::Cdna4};
+    }
+    // MetalFfnFile::offset (metal_ffn.cpp:300-305): byte offset of a tensor.
+    uint64_t offset(const Tensor &t) const { return entry(t).first; }
+    Layout layout(const Tensor &t) const { return entry(t).second; }
+    const void *data(const Tensor &t) const { return static_cast<const uint8_t *>(base_) + offset(t); }
+
+private:
+    const std::pair<uint64_t, Layout> &entry(const Tensor &t) const {
+        const auto it = entries_.find(t.offset);
+        if (it == entries_.end()) throw std::runtime_error("tensor missing from weight image: " + t.name);
+        return it->second;
+    }
+    void *base_ = nullptr;
+    size_t size_ = 0;
+    std::unordered_map<uint64_t, std::pair<uint64_t, Layout>> entries_;
+};
+
+// The FFN dispatch helpers of the reference engine over one device context.
+class FfnPath {
+public:
+    explicit FfnPath(const WeightImage &weights, int device = 0) : w_(weights) { check(ns_ctx_create(device, &ctx_)); }
+    ~FfnPath() { ns_ctx_destroy(ctx_); }
+    FfnPath(const FfnPath &) = delete;
+    FfnPath &operator=(const FfnPath &) = delete;
+
+    // mm:269-275: batch 1 -> dequant-fused GEMV; batch > 1 with fp16 input ->
+    // MFMA GEMM (FP32 accumulation); batch > 1 with fp32 input -> per-token GEMV.
+    void matmul(hipStream_t e, const Tensor &w, const void *in, float *out, uint32_t batch,
+                bool half_input = false) const {
+        check(ns_matmul(ctx_, w_.data(w), int(w.type), int(w_.layout(w)), cols(w), rows(w), batch, in,
+                        half_input ? 1 : 0, out, e));
+    }
+    // mm:288: prefill gate/up + GeGLU, fp16 in, fp16 out; fast_swa selects the FP16 mode.
+    void gate_up_geglu_rm32(hipStream_t e, const Tensor &gate, const Tensor &up, const uint16_t *in, uint16_t *out,
+                            uint32_t batch, bool fast_swa) const {
+        same_shape(gate, up);
+        check(ns_gate_up_geglu_rm32(ctx_, w_.data(gate), w_.data(up), int(w_.layout(gate)), cols(gate), rows(gate),
+                                    batch, in, out, fast_swa ? 1 : 0, e));
+    }
+    // mm:290: decode gate/up + GeGLU, fp32 in and out.
+    void gate_up_geglu_decode(hipStream_t e, const Tensor &gate, const Tensor &up, const float *in, float *out) const {
+        same_shape(gate, up);
+        check(ns_gate_up_geglu_decode(ctx_, w_.data(gate), w_.data(up), int(w_.layout(gate)), cols(gate), rows(gate),
+                                      in, out, e));
+    }
+    // mm:289: the down projection; prefill GEMM when half_input and batch > 1.
+    void ffn_down(hipStream_t e, const Tensor &w, const void *in, float *out, uint32_t batch, bool half_input,
+                  bool fast_swa = false) const {
+        check(ns_ffn_down(ctx_, w_.data(w), int(w.type), int(w_.layout(w)), cols(w), rows(w), batch, in,
+                          half_input ? 1 : 0, fast_swa ? 1 : 0, out, e));
+    }
+
+private:
+    static uint32_t cols(const Tensor &t) { return uint32_t(t.shape.at(0)); }
+    static uint32_t rows(const Tensor &t) { return t.shape.size() > 1 ? uint32_t(t.shape[1]) : 1u; }
+    void same_shape(const Tensor &a, const Tensor &b) const {
+        if (a.shape != b.shape || w_.layout(a) != w_.layout(b))
+            throw std::runtime_error("gate and up tensors differ in shape or layout: " + a.name + ", " + b.name);
+    }
+    const WeightImage &w_;
+    ns_ctx *ctx_ = nullptr;
+};
+
+}  // namespace neutron::amd

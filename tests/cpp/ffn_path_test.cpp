@@ -1,0 +1,154 @@
+// ffn_path_test.cpp -- drives the C++ host layer (neutron-star_amd/host/ffn_path.hpp)
+// the way the reference engine drives its FFN helpers (metal_engine.mm:562-576):
+// decode FFN block + lm-head, then a prefill FFN block in both accumulation
+// modes, each checked against the CPU oracle; then the error convention
+// (std::runtime_error).  Exit status 0 = pass.  Built by __graft_entry__.build()
+// and run by tests/test_gpu_cpp_path.py on the GPU.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <stdexcept>
+#include <vector>
+
+#include "ffn_path.hpp"
+#include "ns_oracle.h"
+
+using namespace neutron::amd;
+
+namespace {
+int failures = 0;
+
+void expect(bool ok, const char *what) {
+    std::printf("%s: %s\n", ok ? "ok  " : "FAIL", what);
+    if (!ok) ++failures;
+}
+
+// max over rows of max|got-ref| / max|ref|
+double rel_err(const std::vector<float> &got, const std::vector<float> &ref, size_t rows, size_t cols) {
+    double worst = 0;
+    for (size_t r = 0; r < rows; ++r) {
+        double num = 0, den = 1e-30;
+        for (size_t c = 0; c < cols; ++c) {
+            num = std::fmax(num, std::fabs(double(got[r * cols + c]) - ref[r * cols + c]));
+            den = std::fmax(den, std::fabs(double(ref[r * cols + c])));
+        }
+        worst = std::fmax(worst, num / den);
+    }
+    return worst;
+}
+
+std::vector<uint8_t> synth(TensorType t, uint64_t seed, uint64_t rows, uint64_t cols) {
+    const size_t bs = t == TensorType::Q4_K ? 144 : 210;
+    std::vector<uint8_t> v(rows * (cols / 256) * bs);
+    check(ns_synth_blocks(int(t), seed, 0, rows * (cols / 256), v.data(), 4));
+    return v;
+}
+
+template <class T>
+T *dev(const std::vector<T> &h) {
+    T *p = nullptr;
+    if (hipMalloc(&p, h.size() * sizeof(T)) != hipSuccess) throw std::runtime_error("hipMalloc");
+    if (hipMemcpy(p, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice) != hipSuccess)
+        throw std::runtime_error("hipMemcpy");
+    return p;
+}
+template <class T>
+std::vector<T> host(const T *p, size_t n) {
+    std::vector<T> h(n);
+    if (hipMemcpy(h.data(), p, n * sizeof(T), hipMemcpyDeviceToHost) != hipSuccess) throw std::runtime_error("hipMemcpy");
+    return h;
+}
+}  // namespace
+
+int main() {
+    const uint64_t D = 768, F = 512, V = 1024, B = 70;
+    hipStream_t s = nullptr;
+    if (hipStreamCreate(&s) != hipSuccess) return 2;
+
+    // Tensors as the engine sees them: gate/up Q4_K [F][D], down Q6_K [D][F],
+    // token embedding (lm-head) Q6_K [V][D] row-major.
+    Tensor gate{"blk.0.ffn_gate.weight", {D, F}, TensorType::Q4_K, 0, F * (D / 256) * 144};
+    Tensor up{"blk.0.ffn_up.weight", {D, F}, TensorType::Q4_K, 1, F * (D / 256) * 144};
+    Tensor down{"blk.0.ffn_down.weight", {F, D}, TensorType::Q6_K, 2, D * (F / 256) * 210};
+    Tensor embd{"token_embd.weight", {D, V}, TensorType::Q6_K, 3, V * (D / 256) * 210};
+    const auto hg = synth(gate.type, 11, F, D), hu = synth(up.type, 12, F, D);
+    const auto hd = synth(down.type, 13, D, F), he = synth(embd.type, 14, V, D);
+    // the FFN tensors arrive in the .nsmffn order (as neutron-convert-metal-ffn writes them)
+    auto nsm = [&](const std::vector<uint8_t> &rm, const Tensor &t) {
+        std::vector<uint8_t> o(rm.size());
+        check(ns_retile(rm.data(), o.data(), int(t.type), uint32_t(t.shape[0]), uint32_t(t.shape[1]),
+                        NS_LAYOUT_ROW_MAJOR, NS_LAYOUT_NSMFFN));
+        return o;
+    };
+    WeightImage img;
+    uint64_t off[4], total = 0;
+    for (int i = 0; i < 4; ++i) {
+        off[i] = total;
+        const Tensor &t = i == 0 ? gate : i == 1 ? up : i == 2 ? down : embd;
+        total += (t.bytes + 255) / 256 * 256;
+    }
+    img.allocate(total);
+    img.upload(gate, nsm(hg, gate).data(), off[0], Layout::Nsmffn, true, s);
+    img.upload(up, nsm(hu, up).data(), off[1], Layout::Nsmffn, true, s);
+    img.upload(down, nsm(hd, down).data(), off[2], Layout::Nsmffn, true, s);
+    img.upload(embd, he.data(), off[3], Layout::RowMajor, false, s);
+    expect(img.layout(gate) == Layout::Cdna4 && img.layout(embd) == Layout::RowMajor, "conversion at load time");
+    FfnPath path(img);
+
+    // ---- decode (mm:571-576): gate/up GeGLU, down GEMV, lm-head GEMV
+    std::vector<float> x(D), xe(D);
+    check(ns_synth_normal_f32(21, 0, D, x.data(), 4));
+    check(ns_synth_normal_f32(22, 0, D, xe.data(), 4));
+    float *dx = dev(x), *dxe = dev(xe), *dh = dev(std::vector<float>(F)), *dy = dev(std::vector<float>(D));
+    float *dl = dev(std::vector<float>(V));
+    path.gate_up_geglu_decode(s, gate, up, dx, dh);
+    path.ffn_down(s, down, dh, dy, 1, false);
+    path.matmul(s, embd, dxe, dl, 1);
+    if (hipStreamSynchronize(s) != hipSuccess) return 3;
+    const auto h = host(dh, F), y = host(dy, D), l = host(dl, V);
+    std::vector<float> h_ref(F), y_ref(D), l_ref(V);
+    nso_gate_up_geglu(NSO_ROW_MAJOR, hg.data(), hu.data(), D, F, x.data(), h_ref.data(), 4);
+    nso_gemv(NSO_Q6_K, NSO_ROW_MAJOR, hd.data(), F, D, h.data(), y_ref.data(), 4);
+    nso_gemv(NSO_Q6_K, NSO_ROW_MAJOR, he.data(), D, V, xe.data(), l_ref.data(), 4);
+    expect(rel_err(h, h_ref, 1, F) <= 1e-3, "decode gate/up GeGLU within 1e-3");
+    expect(rel_err(y, y_ref, 1, D) <= 1e-3, "decode down GEMV within 1e-3");
+    expect(rel_err(l, l_ref, 1, V) <= 1e-3, "lm-head GEMV (row-major) within 1e-3");
+
+    // ---- prefill (mm:563-573), both accumulation modes
+    std::vector<uint16_t> xp(B * D);
+    check(ns_synth_normal_f16(23, 0, B * D, xp.data(), 4));
+    uint16_t *dxp = dev(xp), *dhp = dev(std::vector<uint16_t>(B * F));
+    float *dyp = dev(std::vector<float>(B * D));
+    for (int fast = 0; fast < 2; ++fast) {
+        path.gate_up_geglu_rm32(s, gate, up, dxp, dhp, uint32_t(B), fast != 0);
+        path.ffn_down(s, down, dhp, dyp, uint32_t(B), true, fast != 0);
+        if (hipStreamSynchronize(s) != hipSuccess) return 3;
+        const auto hp16 = host(dhp, B * F);
+        const auto yp = host(dyp, B * D);
+        std::vector<float> hp(B * F), hp_ref(B * F), yp_ref(B * D);
+        for (size_t i = 0; i < hp.size(); ++i) hp[i] = nso_f16_to_f32(hp16[i]);
+        nso_gate_up_geglu_prefill(NSO_ROW_MAJOR, hg.data(), hu.data(), D, F, B, xp.data(), 0, hp_ref.data(), 4);
+        nso_gemm(NSO_Q6_K, NSO_ROW_MAJOR, hd.data(), F, D, B, hp16.data(), 0, yp_ref.data(), 4);
+        const double tol = fast ? 1e-2 : 1e-3;
+        expect(rel_err(hp, hp_ref, B, F) <= tol, fast ? "prefill gate/up FP16 mode within 1e-2" : "prefill gate/up FP32 mode within 1e-3");
+        expect(rel_err(yp, yp_ref, B, D) <= tol, fast ? "prefill down FP16 mode within 1e-2" : "prefill down FP32 mode within 1e-3");
+    }
+
+    // ---- errors surface as std::runtime_error (mm:231-243 convention)
+    Tensor missing{"blk.9.ffn_up.weight", {D, F}, TensorType::Q4_K, 99, 0};
+    bool threw = false;
+    try { path.matmul(s, missing, dx, dh, 1); } catch (const std::runtime_error &) { threw = true; }
+    expect(threw, "unknown tensor throws");
+    threw = false;
+    try { path.gate_up_geglu_decode(s, gate, down, dx, dh); } catch (const std::runtime_error &) { threw = true; }
+    expect(threw, "gate/up shape mismatch throws");
+    threw = false;
+    try { path.matmul(s, gate, dx, dh, 0); } catch (const std::runtime_error &e) { threw = std::strstr(e.what(), "batch") != nullptr; }
+    expect(threw, "zero batch throws with the C ABI message");
+
+    (void)hipFree(dx); (void)hipFree(dxe); (void)hipFree(dh); (void)hipFree(dy); (void)hipFree(dl);
+    (void)hipFree(dxp); (void)hipFree(dhp); (void)hipFree(dyp);
+    (void)hipStreamDestroy(s);
+    std::printf("%s (%d failures)\n", failures ? "FAILED" : "PASSED", failures);
+    return failures ? 1 : 0;
+}
