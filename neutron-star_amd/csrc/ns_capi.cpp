@@ -72,7 +72,7 @@ int ensure_ws(ns_ctx *ctx, size_t partial_floats, size_t counters) {
 int gemv(ns_ctx *ctx, const char *fn, int type, int layout, const void *w, const void *up, const float *x,
          float *out, uint32_t cols, uint32_t rows, hipStream_t s) {
     size_t pf = 0, nc = 0;
-    gemv_workspace_need(cols, rows, up != nullptr, &pf, &nc);
+    gemv_workspace_need(type, layout, cols, rows, up != nullptr, &pf, &nc);
     if (int rc = ensure_ws(ctx, pf, nc)) return rc;
     const hipError_t e = launch_gemv(type, layout, static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(up),
                                      x, out, cols, rows, ctx->ws, s);

@@ -5,17 +5,19 @@
 // matmul batch==1 at metal_engine.mm:272 and gate_up_geglu_decode at mm:290).
 //
 // Work decomposition (wave64, lane = weight row):
-//   * one workgroup owns a 64-row slab (the .nsmffn row tile) and a contiguous
-//     run of that slab's super-blocks; each of its waves takes a sub-run;
+//   * the work is the flattened sequence of (64-row slab, super-block) units;
+//     the grid holds as many workgroups as the device keeps resident, each
+//     takes an equal contiguous run of units and splits it evenly over its
+//     waves, so every wave streams the same number of weight bytes;
 //   * every lane streams its own row's blocks: in the CDNA4 layout each of the
 //     9 (Q4_K) or 13 (Q6_K) 16-byte chunk loads of a wave is one contiguous
-//     1 KiB transaction; the next block is prefetched while one is computed;
+//     1 KiB transaction; the next unit is prefetched while one is computed;
 //   * x is wave-uniform (every lane needs the same 256 values of a block) and
 //     is read with scalar loads; per-group sums of x are built across lanes;
-//   * partial sums meet in LDS (fixed wave order); when a slab's super-blocks
-//     are split over several workgroups, each writes its partial to the
-//     context workspace and the last one to arrive sums them in chunk order,
-//     so results are deterministic.
+//   * a wave writes the slabs it covers whole; slabs cut between waves meet in
+//     LDS in wave order, and slabs cut between workgroups are finished by the
+//     last workgroup to arrive, which adds the parts in workgroup order, so
+//     results are deterministic.
 //
 // Per super-block the Q4_K dot is factorised as in the reference's
 // q4k_mv_block_fast (metal:73):  sum_k w_k x_k = d * sum_g sc_g (sum_l q x)
@@ -29,7 +31,7 @@
 namespace ns {
 namespace {
 
-constexpr int kMaxWaves = 8;
+constexpr uint32_t kWgWaves = 4;  // waves per workgroup
 
 // ---- block loads --------------------------------------------------------
 
@@ -128,8 +130,15 @@ __device__ __forceinline__ void q4_dot(const u32x4 (&c)[N][kQ4Chunks], const flo
     }
 }
 
-// Q6_K (quant.cpp:13-18): element (half h, quarter q, l) uses scale 8h + l/16 + 2q;
-// sum (v-32) x = sum v x - 32 sum x over each 16-wide scale group.
+// Q6_K (quant.cpp:13-18): element (half h, quarter q, l) of a super-block is
+// v = nibble of ql[64h + 32(q&1) + l] (low for q < 2) | ((qh[32h + l] >> 2q) & 3) << 4
+// and uses scale 8h + 2q + l/16; sum (v-32) x = sum v x - 32 sum x over each
+// 16-wide scale group.  The 6-bit v are assembled directly as fp16 subnormals
+// (as for Q4_K): for the even bytes of a dword, (ql & 0x000F000F) | (qh<<4 &
+// 0x00300030) is v * 2^-24 in both halves (quarter 0), and (ql & 0x00F000F0) |
+// (qh<<4 & 0x03000300) is v * 2^-20 (quarter 2); quarters 1 and 3 take qh<<2
+// and the ql dword at l+32; the odd bytes repeat this on the operands shifted
+// right by 8.  22 integer operations then feed 16 mixed-precision FMAs.
 __device__ __forceinline__ float q6_dot(const u32x4 (&c)[kQ6Chunks], uint32_t dbits,
                                         const float *__restrict__ xb, const float (&xs)[16]) {
     const float d = lo_half(dbits);
@@ -142,23 +151,36 @@ __device__ __forceinline__ float q6_dot(const u32x4 (&c)[kQ6Chunks], uint32_t db
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const Q6Quarters q = q6_quarters(comp(c[4 * h + t], u), comp(c[4 * h + 2 + t], u),
-                                                 comp(c[8 + 2 * h + t], u));
-                const int l = 16 * t + 4 * u;
-                const float *x0 = xb + 128 * h + l;
+                const uint32_t a = comp(c[4 * h + t], u), b = comp(c[4 * h + 2 + t], u);
+                const uint32_t hq = comp(c[8 + 2 * h + t], u);
+                const float *x0 = xb + 128 * h + 16 * t + 4 * u;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    A[8 * h + t + 0] = __builtin_fmaf(float(byte_of(q.v0, i)), x0[i], A[8 * h + t + 0]);
-                    A[8 * h + t + 2] = __builtin_fmaf(float(byte_of(q.v1, i)), x0[32 + i], A[8 * h + t + 2]);
-                    A[8 * h + t + 4] = __builtin_fmaf(float(byte_of(q.v2, i)), x0[64 + i], A[8 * h + t + 4]);
-                    A[8 * h + t + 6] = __builtin_fmaf(float(byte_of(q.v3, i)), x0[96 + i], A[8 * h + t + 6]);
+                for (int odd = 0; odd < 2; ++odd) {
+                    const uint32_t aa = odd ? a >> 8 : a, bb = odd ? b >> 8 : b;
+                    const uint32_t h4 = odd ? hq >> 4 : hq << 4, h2 = odd ? hq >> 6 : hq << 2;
+                    const uint32_t e0 = (aa & 0x000F000Fu) | (h4 & 0x00300030u);
+                    const uint32_t e2 = (aa & 0x00F000F0u) | (h4 & 0x03000300u);
+                    const uint32_t e1 = (bb & 0x000F000Fu) | (h2 & 0x00300030u);
+                    const uint32_t e3 = (bb & 0x00F000F0u) | (h2 & 0x03000300u);
+                    const float *xo = x0 + odd;  // elements l+odd (lo half) and l+odd+2 (hi half)
+                    float &g0 = A[8 * h + 0 + t], &g1 = A[8 * h + 2 + t], &g2 = A[8 * h + 4 + t], &g3 = A[8 * h + 6 + t];
+                    g0 = __builtin_fmaf(lo_half(e0), xo[0], g0);
+                    g0 = __builtin_fmaf(hi_half(e0), xo[2], g0);
+                    g1 = __builtin_fmaf(lo_half(e1), xo[32], g1);
+                    g1 = __builtin_fmaf(hi_half(e1), xo[34], g1);
+                    g2 = __builtin_fmaf(lo_half(e2), xo[64], g2);
+                    g2 = __builtin_fmaf(hi_half(e2), xo[66], g2);
+                    g3 = __builtin_fmaf(lo_half(e3), xo[96], g3);
+                    g3 = __builtin_fmaf(hi_half(e3), xo[98], g3);
                 }
             }
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
+        // group i = 8h + 2q + t: quarters 0, 1 carry 2^-24, quarters 2, 3 carry 2^-20
+        const float f = ((i >> 1) & 3) >= 2 ? 1048576.0f : 16777216.0f;
         const float sc = float(int8_t(byte_of(comp(c[12], i >> 2), i & 3)));
-        s = __builtin_fmaf(sc, __builtin_fmaf(-32.0f, xs[i], A[i]), s);
+        s = __builtin_fmaf(sc, __builtin_fmaf(A[i], f, -32.0f * xs[i]), s);
     }
     return d * s;
 }
@@ -178,160 +200,289 @@ __device__ __forceinline__ void group_sums(const float *__restrict__ xb, uint32_
         xs[g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), g * (GROUP / 4)));
 }
 
+// Flattened work: unit i = (slab i / nb, super-block i % nb), i < U = nslabs * nb.
+// Workgroup g of G takes units [first(g), first(g+1)) with first(g) = g*q +
+// min(g, r), q = U / G, r = U % G, and splits them evenly over its kWgWaves
+// waves, so every wave streams the same amount of weights.  A wave writes the
+// slabs it covers whole.  Parts of slabs cut between waves meet in LDS (wave
+// order); a slab cut between workgroups is finished by the last of its
+// workgroups to arrive, which adds the workgroup parts in workgroup order.
+// Results therefore do not depend on timing.
+struct Split {
+    uint32_t q, r;
+    __device__ __forceinline__ uint32_t first(uint32_t g) const { return g * q + __builtin_elementwise_min(g, r); }
+    // the workgroup whose range holds unit i
+    __device__ __forceinline__ uint32_t owner(uint32_t i) const {
+        const uint32_t big = r * (q + 1);
+        return i < big ? i / (q + 1) : r + (i - big) / q;
+    }
+};
+
 template <int TYPE, int LAYOUT, bool PAIR>
-__global__ __launch_bounds__(kMaxWaves * 64) void gemv_kernel(
+__global__ __launch_bounds__(kWgWaves * 64) void gemv_kernel(
     const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, const float *__restrict__ x,
-    float *__restrict__ out, uint32_t rows, uint32_t nb, uint32_t kchunks, uint32_t nranges,
-    float *__restrict__ partial, uint32_t *__restrict__ counters) {
+    float *__restrict__ out, uint32_t rows, uint32_t nb, uint32_t nslabs, float *__restrict__ partial,
+    uint32_t *__restrict__ counters) {
+    constexpr uint32_t kPlanes = PAIR ? 2 : 1;
+    __shared__ float lds_part[kWgWaves][2][kPlanes][64];
+    __shared__ uint32_t lds_slab[kWgWaves][2];
+
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t nwaves = blockDim.x >> 6;
-    const uint32_t slab = blockIdx.x / kchunks, kc = blockIdx.x - slab * kchunks;
-    const uint32_t row = slab * kRowTile + lane;
-    const bool valid = row < rows;
-    const uint32_t ri = kc * nwaves + wave;
-    const uint32_t b0 = ri * nb / nranges, b1 = (ri + 1) * nb / nranges;
+    const uint32_t G = gridDim.x, g = blockIdx.x, U = nslabs * nb;
+    const Split sp{U / G, U % G};
+    const uint32_t wg0 = sp.first(g), wg1 = sp.first(g + 1), n = wg1 - wg0;
+    const uint32_t i0 = wg0 + wave * n / kWgWaves, i1 = wg0 + (wave + 1) * n / kWgWaves;
 
+    if (lane < 2) lds_slab[wave][lane] = ~0u;
     float acc0 = 0.f, acc1 = 0.f;
-    if constexpr (TYPE == Q4_K) {
-        constexpr int N = PAIR ? 2 : 1;
-        const uint8_t *wm[2] = {w0, w1};
-        u32x4 c[N][kQ4Chunks];
-        if (valid && b0 < b1)
-#pragma unroll
-            for (int n = 0; n < N; ++n) q4_load<LAYOUT>(wm[n], lane, row, slab, b0, nb, c[n]);
-        for (uint32_t b = b0; b < b1; ++b) {
-            u32x4 nx[N][kQ4Chunks];
-            if (valid && b + 1 < b1)
-#pragma unroll
-                for (int n = 0; n < N; ++n) q4_load<LAYOUT>(wm[n], lane, row, slab, b + 1, nb, nx[n]);
-            const float *xb = x + size_t(b) * kQK;
-            float xs[8], r[N];
-            group_sums<32>(xb, lane, xs);
-            q4_dot<N>(c, xb, xs, r);
-            acc0 += r[0];
-            if constexpr (PAIR) acc1 += r[N - 1];
-#pragma unroll
-            for (int n = 0; n < N; ++n)
-#pragma unroll
-                for (int i = 0; i < int(kQ4Chunks); ++i) c[n][i] = nx[n][i];
-        }
-    } else {
-        u32x4 c0[kQ6Chunks];
-        uint32_t d0 = 0;
-        if (valid && b0 < b1) q6_load<LAYOUT>(w0, lane, row, slab, b0, nb, c0, d0);
-        for (uint32_t b = b0; b < b1; ++b) {
-            u32x4 n0[kQ6Chunks];
-            uint32_t dn = 0;
-            if (valid && b + 1 < b1) q6_load<LAYOUT>(w0, lane, row, slab, b + 1, nb, n0, dn);
-            const float *xb = x + size_t(b) * kQK;
-            float xs[16];
-            group_sums<16>(xb, lane, xs);
-            acc0 += q6_dot(c0, d0, xb, xs);
-#pragma unroll
-            for (int i = 0; i < int(kQ6Chunks); ++i) c0[i] = n0[i];
-            d0 = dn;
-        }
-    }
+    uint32_t slab = i0 / nb, b = i0 - slab * nb, seg_b0 = b, segi = 0;
 
-    __shared__ float red[PAIR ? 2 : 1][kMaxWaves][64];
-    red[0][wave][lane] = acc0;
-    if constexpr (PAIR) red[PAIR ? 1 : 0][wave][lane] = acc1;
-    __syncthreads();
-    if (wave != 0) return;
-    float s0 = 0.f, s1 = 0.f;
-    for (uint32_t w = 0; w < nwaves; ++w) {
-        s0 += red[0][w][lane];
-        if constexpr (PAIR) s1 += red[PAIR ? 1 : 0][w][lane];
-    }
-    if (kchunks > 1) {
-        // Hand-off between workgroups through device-coherent (agent-scope)
-        // atomic stores and loads only: the partials bypass the XCD-private L2,
-        // so no L2-wide write-back/invalidate fence is needed.  The wait below
-        // makes every partial store complete before the arrival is counted;
-        // the last arrival reads them after its counter atomic has returned.
-        if (valid) {
-            __hip_atomic_store(&partial[size_t(kc) * rows + row], s0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if constexpr (PAIR)
-                __hip_atomic_store(&partial[size_t(kchunks + kc) * rows + row], s1, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_s_waitcnt(0);
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        uint32_t prev = 0;
-        if (lane == 0)
-            prev = __hip_atomic_fetch_add(&counters[slab], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        prev = __shfl(prev, 0);
-        if (prev != kchunks - 1) return;
-        s0 = 0.f;
-        s1 = 0.f;
-        if (valid)
-            for (uint32_t k = 0; k < kchunks; ++k) {
-                s0 += __hip_atomic_load(&partial[size_t(k) * rows + row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if constexpr (PAIR)
-                    s1 += __hip_atomic_load(&partial[size_t(kchunks + k) * rows + row], __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
+    // Segment (slab, blocks seg_b0..b) done: write it if whole, else park it in LDS.
+    auto step_done = [&](uint32_t i) {
+        if (b == nb - 1 || i + 1 == i1) {
+            if (seg_b0 == 0 && b == nb - 1) {
+                const uint32_t row = slab * kRowTile + lane;
+                if (row < rows) {
+                    if constexpr (PAIR) out[row] = gelu_tanh(acc0) * acc1;
+                    else out[row] = acc0;
+                }
+            } else {
+                lds_part[wave][segi][0][lane] = acc0;
+                if constexpr (PAIR) lds_part[wave][segi][kPlanes - 1][lane] = acc1;
+                if (lane == 0) lds_slab[wave][segi] = slab;
+                segi = 1;
             }
-        if (lane == 0) __hip_atomic_store(&counters[slab], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (!valid) return;
-    if constexpr (PAIR) out[row] = gelu_tanh(s0) * s1;
-    else out[row] = s0;
-}
+            acc0 = 0.f;
+            acc1 = 0.f;
+            seg_b0 = 0;
+        }
+    };
+    // Rows past `rows` (ROW_MAJOR tails only) load the last row instead; their results are dropped.
+    auto lrow = [&](uint32_t s) { return __builtin_elementwise_min(s * kRowTile + lane, rows - 1); };
+    auto advance = [&](uint32_t &s, uint32_t &bb) {
+        if (++bb == nb) {
+            bb = 0;
+            ++s;
+        }
+    };
 
-struct GemvPlan {
-    uint32_t nslabs, nwaves, kchunks;
-};
+    if (i0 < i1) {
+        if constexpr (TYPE == Q4_K) {
+            constexpr int N = PAIR ? 2 : 1;
+            const uint8_t *wm[2] = {w0, w1};
+            u32x4 c[N][kQ4Chunks];
+#pragma unroll
+            for (int m = 0; m < N; ++m) q4_load<LAYOUT>(wm[m], lane, lrow(slab), slab, b, nb, c[m]);
+            for (uint32_t i = i0; i < i1; ++i) {
+                uint32_t ns_ = slab, nbk = b;
+                advance(ns_, nbk);
+                u32x4 nx[N][kQ4Chunks];
+                if (i + 1 < i1)
+#pragma unroll
+                    for (int m = 0; m < N; ++m) q4_load<LAYOUT>(wm[m], lane, lrow(ns_), ns_, nbk, nb, nx[m]);
+                const float *xb = x + size_t(b) * kQK;
+                float xs[8], r[N];
+                group_sums<32>(xb, lane, xs);
+                q4_dot<N>(c, xb, xs, r);
+                acc0 += r[0];
+                if constexpr (PAIR) acc1 += r[N - 1];
+                step_done(i);
+                slab = ns_;
+                b = nbk;
+#pragma unroll
+                for (int m = 0; m < N; ++m)
+#pragma unroll
+                    for (int k = 0; k < int(kQ4Chunks); ++k) c[m][k] = nx[m][k];
+            }
+        } else {
+            u32x4 c0[kQ6Chunks];
+            uint32_t d0 = 0;
+            q6_load<LAYOUT>(w0, lane, lrow(slab), slab, b, nb, c0, d0);
+            for (uint32_t i = i0; i < i1; ++i) {
+                uint32_t ns_ = slab, nbk = b;
+                advance(ns_, nbk);
+                u32x4 n0[kQ6Chunks];
+                uint32_t dn = 0;
+                if (i + 1 < i1) q6_load<LAYOUT>(w0, lane, lrow(ns_), ns_, nbk, nb, n0, dn);
+                const float *xb = x + size_t(b) * kQK;
+                float xs[16];
+                group_sums<16>(xb, lane, xs);
+                acc0 += q6_dot(c0, d0, xb, xs);
+                step_done(i);
+                slab = ns_;
+                b = nbk;
+#pragma unroll
+                for (int k = 0; k < int(kQ6Chunks); ++k) c0[k] = n0[k];
+                d0 = dn;
+            }
+        }
+    }
+    if (n == 0) return;
+    const uint32_t s_lo = wg0 / nb, s_hi = (wg1 - 1) / nb;
+    // Slabs parked in LDS: at most the workgroup's first and last slab (cut
+    // between workgroups) and slabs cut only between its own waves.
+    __syncthreads();
+    for (uint32_t s = s_lo + wave; s <= s_hi; s += kWgWaves) {
+        float r0 = 0.f, r1 = 0.f;
+        bool any = false;
+        for (uint32_t v = 0; v < kWgWaves; ++v)
+#pragma unroll
+            for (uint32_t k = 0; k < 2; ++k)
+                if (lds_slab[v][k] == s) {
+                    r0 += lds_part[v][k][0][lane];
+                    if constexpr (PAIR) r1 += lds_part[v][k][kPlanes - 1][lane];
+                    any = true;
+                }
+        if (!any) continue;  // whole slab, already written
+        const uint32_t row = s * kRowTile + lane;
+        const bool cut = s * nb < wg0 || (s + 1) * nb > wg1;
+        if (cut) {
+            // Device-coherent (agent-scope) atomic stores and loads only: the
+            // parts bypass the XCD-private L2, so no L2-wide fence is needed.
+            // The wait makes the part stores complete before the arrival is
+            // counted; the last arrival reads the parts after its atomic returned.
+            const uint32_t slot = s == s_lo ? 0u : 1u;
+            float *dst = partial + (size_t(g) * 2 + slot) * (kPlanes * 64);
+            __hip_atomic_store(&dst[lane], r0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if constexpr (PAIR) __hip_atomic_store(&dst[64 + lane], r1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_s_waitcnt(0);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            const uint32_t gf = sp.owner(s * nb), gl = sp.owner(s * nb + nb - 1);
+            uint32_t prev = 0;
+            if (lane == 0) prev = __hip_atomic_fetch_add(&counters[s], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            prev = __builtin_amdgcn_readfirstlane(__shfl(prev, 0));
+            if (prev != gl - gf) continue;
+            r0 = 0.f;
+            r1 = 0.f;
+            // Parts of workgroups gf..gl, loaded 8 at a time and added in order.
+            for (uint32_t h0 = gf; h0 <= gl; h0 += 8) {
+                float v0[8], v1[8];
+#pragma unroll
+                for (uint32_t j = 0; j < 8; ++j) {
+                    const uint32_t h = __builtin_elementwise_min(h0 + j, gl);
+                    // workgroup h's part of slab s is its first slot unless h began in an earlier slab
+                    const uint32_t si = sp.first(h) < s * nb ? 1u : 0u;
+                    const float *p = partial + (size_t(h) * 2 + si) * (kPlanes * 64);
+                    v0[j] = __hip_atomic_load(&p[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    v1[j] = PAIR ? __hip_atomic_load(&p[64 + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+                }
+#pragma unroll
+                for (uint32_t j = 0; j < 8; ++j)
+                    if (h0 + j <= gl) {
+                        r0 += v0[j];
+                        r1 += v1[j];
+                    }
+            }
+            if (lane == 0) __hip_atomic_store(&counters[s], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (row < rows) {
+            if constexpr (PAIR) out[row] = gelu_tanh(r0) * r1;
+            else out[row] = r0;
+        }
+    }
+}
 
 int env_int(const char *name, int dflt) {
     const char *v = getenv(name);
     return v && *v ? atoi(v) : dflt;
 }
 
-// Splits each slab's nb super-blocks into nwaves*kchunks runs, aiming at
-// ~4096 waves in flight (16 per CU on 256 CUs) with runs of >= 1 block.
-GemvPlan plan_gemv(uint32_t cols, uint32_t rows) {
+template <int TYPE, int LAYOUT, bool PAIR>
+constexpr auto kernel_of() {
+    return &gemv_kernel<TYPE, LAYOUT, PAIR>;
+}
+
+// Resident waves per CU of one kernel instance, and the CU count, per device.
+struct DeviceShape {
+    int cus = 0;
+};
+DeviceShape device_shape() {
+    static DeviceShape cache[64];
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    DeviceShape &d = cache[dev & 63];
+    if (d.cus == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+        d.cus = cus;
+    }
+    return d;
+}
+
+template <int TYPE, int LAYOUT, bool PAIR>
+int waves_per_cu() {
+    static int cache[64] = {};
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    int &w = cache[dev & 63];
+    if (w == 0) {
+        int wgs = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&wgs, kernel_of<TYPE, LAYOUT, PAIR>(), kWgWaves * 64, 0) !=
+                hipSuccess || wgs <= 0)
+            wgs = 2;
+        w = wgs * kWgWaves;
+    }
+    return w;
+}
+
+struct GemvPlan {
+    uint32_t nslabs, G;  // G workgroups of kWgWaves waves
+};
+
+// G: as many workgroups as the device holds at once (never more than there
+// are units).  Measured on MI355X this is at or near the best grid for every
+// shape of the path: the 262144-row lm-head (4096 slabs, 1.3 slabs per wave),
+// the 3840-row down projection and the 15360-row gate/up projections.
+GemvPlan plan_gemv(uint32_t cols, uint32_t rows, int resident_waves) {
     GemvPlan p;
     const uint32_t nb = cols / kQK;
     p.nslabs = (rows + kRowTile - 1) / kRowTile;
-    uint32_t want = (4096 + p.nslabs - 1) / p.nslabs;
-    want = want < 1 ? 1 : (want > nb ? nb : want);
-    p.kchunks = (want + kMaxWaves - 1) / kMaxWaves;
-    p.nwaves = (want + p.kchunks - 1) / p.kchunks;
-    while (p.nwaves * p.kchunks > nb && p.nwaves > 1) --p.nwaves;
-    const int ew = env_int("NS_GEMV_WAVES", 0), ek = env_int("NS_GEMV_KCHUNKS", 0);
-    if (ew > 0 && ew <= kMaxWaves) p.nwaves = uint32_t(ew);
-    if (ek > 0) p.kchunks = uint32_t(ek);
-    while (p.nwaves * p.kchunks > nb) {
-        if (p.kchunks > 1) --p.kchunks;
-        else --p.nwaves;
-    }
+    const uint32_t U = p.nslabs * nb;
+    uint32_t cap = uint32_t(resident_waves > 0 ? resident_waves : 2048);
+    if (const int e = env_int("NS_GEMV_WAVES", 0); e > 0) cap = uint32_t(e);
+    p.G = (cap + kWgWaves - 1) / kWgWaves;
+    if (p.G > U) p.G = U;
     return p;
+}
+
+template <int TYPE, bool PAIR>
+int resident_waves(int layout) {
+    const int cus = device_shape().cus;
+    if (layout == CDNA4) return cus * waves_per_cu<TYPE, CDNA4, PAIR>();
+    if (layout == NSMFFN) return cus * waves_per_cu<TYPE, NSMFFN, PAIR>();
+    return cus * waves_per_cu<TYPE, ROW_MAJOR, PAIR>();
+}
+
+int resident_waves_for(int type, int layout, bool pair) {
+    if (pair) return resident_waves<Q4_K, true>(layout);
+    if (type == Q4_K) return resident_waves<Q4_K, false>(layout);
+    return resident_waves<Q6_K, false>(layout);
 }
 
 template <int TYPE, bool PAIR>
 hipError_t launch_typed(int layout, const uint8_t *w, const uint8_t *up, const float *x, float *out,
                         uint32_t cols, uint32_t rows, const Workspace &ws, hipStream_t stream) {
-    const GemvPlan p = plan_gemv(cols, rows);
+    const GemvPlan p = plan_gemv(cols, rows, resident_waves<TYPE, PAIR>(layout));
     const uint32_t nb = cols / kQK;
-    const dim3 grid(p.nslabs * p.kchunks), block(p.nwaves * 64);
-    const uint32_t nr = p.nwaves * p.kchunks;
+    const dim3 grid(p.G), block(kWgWaves * 64);
     if (layout == CDNA4)
-        gemv_kernel<TYPE, CDNA4, PAIR><<<grid, block, 0, stream>>>(w, up, x, out, rows, nb, p.kchunks, nr, ws.partial, ws.counters);
+        gemv_kernel<TYPE, CDNA4, PAIR><<<grid, block, 0, stream>>>(w, up, x, out, rows, nb, p.nslabs, ws.partial, ws.counters);
     else if (layout == NSMFFN)
-        gemv_kernel<TYPE, NSMFFN, PAIR><<<grid, block, 0, stream>>>(w, up, x, out, rows, nb, p.kchunks, nr, ws.partial, ws.counters);
+        gemv_kernel<TYPE, NSMFFN, PAIR><<<grid, block, 0, stream>>>(w, up, x, out, rows, nb, p.nslabs, ws.partial, ws.counters);
     else
-        gemv_kernel<TYPE, ROW_MAJOR, PAIR><<<grid, block, 0, stream>>>(w, up, x, out, rows, nb, p.kchunks, nr, ws.partial, ws.counters);
+        gemv_kernel<TYPE, ROW_MAJOR, PAIR><<<grid, block, 0, stream>>>(w, up, x, out, rows, nb, p.nslabs, ws.partial, ws.counters);
     return hipGetLastError();
 }
 
 }  // namespace
 
-void gemv_workspace_need(uint32_t cols, uint32_t rows, bool pair, size_t *partial_floats, size_t *counters) {
-    const GemvPlan p = plan_gemv(cols, rows);
-    *partial_floats = p.kchunks > 1 ? size_t(p.kchunks) * rows * (pair ? 2 : 1) : 0;
-    *counters = p.kchunks > 1 ? p.nslabs : 0;
+void gemv_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, bool pair, size_t *partial_floats,
+                         size_t *counters) {
+    const GemvPlan p = plan_gemv(cols, rows, resident_waves_for(type, layout, pair));
+    *partial_floats = size_t(p.G) * 2 * 64 * (pair ? 2 : 1);
+    *counters = p.nslabs;
 }
 
 hipError_t launch_gemv(int type, int layout, const uint8_t *w, const uint8_t *up, const float *x,

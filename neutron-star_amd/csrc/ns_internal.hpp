@@ -29,7 +29,7 @@ hipError_t launch_gemv(int type, int layout, const uint8_t *w, const uint8_t *up
                        const Workspace &ws, hipStream_t stream);
 
 // Required workspace for launch_gemv with these shapes.
-void gemv_workspace_need(uint32_t cols, uint32_t rows, bool pair, size_t *partial_floats,
+void gemv_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, bool pair, size_t *partial_floats,
                          size_t *counters);
 
 // Workspace the prefill GEMM needs: Q4_K group sums of x, split-K parts, tile counters.
