@@ -51,7 +51,15 @@ enum { NS_LAYOUT_ROW_MAJOR = 0, NS_LAYOUT_NSMFFN = 1, NS_LAYOUT_CDNA4 = 2 };
  *         range) at every 256-wide super-block boundary. */
 enum { NS_ACC_FP32 = 0, NS_ACC_FP16 = 1 };
 
-enum { NS_OK = 0, NS_ERR_ARG = 1, NS_ERR_SHAPE = 2, NS_ERR_HIP = 3, NS_ERR_UNSUPPORTED = 4 };
+enum {
+    NS_OK = 0,
+    NS_ERR_ARG = 1,
+    NS_ERR_SHAPE = 2,
+    NS_ERR_HIP = 3,
+    NS_ERR_UNSUPPORTED = 4,
+    NS_ERR_IO = 5,     /* file create/read/write/mmap failure */
+    NS_ERR_FORMAT = 6  /* .nsmffn file does not validate */
+};
 
 typedef struct ns_ctx ns_ctx;
 
@@ -122,6 +130,57 @@ int ns_synth_normal_f16(uint64_t seed, uint64_t first, uint64_t count, uint16_t 
                         int nthreads);
 /* Per-layer seed: seed ^ (layer * 0x9E3779B97F4A7C15). */
 uint64_t ns_layer_seed(uint64_t seed, uint32_t layer);
+
+/* ---- the .nsmffn v3 weight file (host-side; no GPU needed) -------------------
+ *
+ * Byte-compatible with the reference's format (include/neutron/native/metal_ffn.hpp:13-40,
+ * src/native/metal_ffn.cpp): a 64 KiB header page (72-byte header + one 48-byte entry per
+ * GGUF tensor) and every tensor at its GGUF position, FFN tensors re-laid into 64-row slabs. */
+
+/* MetalFfnKind (metal_ffn.hpp:13); NS_FFN_NONE marks a tensor that is not an FFN matrix. */
+enum { NS_FFN_GATE = 0, NS_FFN_UP = 1, NS_FFN_DOWN = 2 };
+#define NS_FFN_NONE 0xFFFFFFFFu
+
+/* One GGUF tensor, in GGUF tensor-table order (gguf.hpp:20-27 plus the layer/kind
+ * that ffn_tensors() assigns from the model, metal_ffn.cpp:63-71). */
+typedef struct ns_tensor_desc {
+    uint64_t source_offset; /* Tensor::offset: byte offset inside the GGUF data section */
+    uint64_t bytes;         /* Tensor::bytes */
+    uint32_t type;          /* GGUF type id (NS_TYPE_Q4_K, NS_TYPE_Q6_K, 0 = F32, 1 = F16, ...) */
+    uint32_t cols, rows;    /* shape[0], shape[1] (1 for vectors) */
+    uint32_t layer;         /* FFN layer index, or NS_FFN_NONE */
+    uint32_t kind;          /* NS_FFN_GATE / _UP / _DOWN, or NS_FFN_NONE */
+    uint32_t reserved;      /* padding to 40 bytes; ignored */
+} ns_tensor_desc;
+
+/* metal_ffn_fingerprint (metal_ffn.cpp:81-90): the FNV-1a 64 loop (prime 1099511628211) from
+ * the reference's start value 1469598103934665603 over version 3 (u32 LE), the GGUF file size
+ * (u64 LE) and the first min(head_bytes, 16 MiB) bytes of the GGUF, where head_bytes is the
+ * GGUF data offset. */
+uint64_t ns_nsmffn_fingerprint(const void *gguf_head, uint64_t head_bytes, uint64_t gguf_file_size);
+
+/* convert_metal_ffn (metal_ffn.cpp:92-165): write out_path (via out_path.tmp, fsync, rename)
+ * from the GGUF image `gguf` (gguf_size bytes, data section at data_offset). */
+int ns_nsmffn_convert(const char *out_path, const void *gguf, uint64_t gguf_size, uint64_t data_offset,
+                      const ns_tensor_desc *tensors, uint32_t count);
+
+/* convert_metal_ffn_in_place (metal_ffn.cpp:167-251): re-lay the FFN tensors of the GGUF file
+ * model_path slab by slab, save its metadata area as a sparse GGUF at metadata_path, then write
+ * the header page over the start of model_path.  Needs data_offset >= 64 KiB. */
+int ns_nsmffn_convert_in_place(const char *model_path, const char *metadata_path, uint64_t data_offset,
+                               const ns_tensor_desc *tensors, uint32_t count);
+
+/* MetalFfnFile (metal_ffn.cpp:253-311): mmap `path` read-only and validate it against the GGUF
+ * it was made from (its size and ns_nsmffn_fingerprint) and its tensor table; NS_ERR_FORMAT
+ * with the reference's messages when it does not match. */
+typedef struct ns_nsmffn ns_nsmffn;
+int ns_nsmffn_open(const char *path, uint64_t gguf_size, uint64_t gguf_fingerprint,
+                   const ns_tensor_desc *expected, uint32_t count, ns_nsmffn **out);
+int ns_nsmffn_close(ns_nsmffn *f);
+const void *ns_nsmffn_data(const ns_nsmffn *f); /* MetalFfnFile::mapped_data */
+uint64_t ns_nsmffn_size(const ns_nsmffn *f);    /* MetalFfnFile::file_size */
+/* MetalFfnFile::offset and ::reordered of the tensor whose GGUF offset is source_offset. */
+int ns_nsmffn_lookup(const ns_nsmffn *f, uint64_t source_offset, uint64_t *offset, int *reordered);
 
 #ifdef __cplusplus
 }

@@ -280,7 +280,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     // PAIR: gate columns 0..127 come from waves with (wave & 3) < 2: wave-uniform
     const rsrc_t wsrc = make_rsrc((PAIR && (wave & 3) >= 2) ? w1 : w0, wbytes);
     const uint32_t wrow = r0 + (PAIR ? (wc % (TC / 2)) : wc);
-    const bool wvalid = wrow < rows;
     const rsrc_t xsrc = make_rsrc(x, batch * cols * 2);
     // x group sums: plane hi [batch][ngroups] then plane lo; rows past batch are
     // never stored, so their (lo-plane) contents do not matter

@@ -17,6 +17,7 @@ HEADER = os.path.join(ROOT, "include", "ns_ffn.h")
 
 Q4_K, Q6_K = 12, 14
 ROW_MAJOR, NSMFFN, CDNA4 = 0, 1, 2
+FFN_GATE, FFN_UP, FFN_DOWN, FFN_NONE = 0, 1, 2, 0xFFFFFFFF
 ACC_FP32, ACC_FP16 = 0, 1
 BLOCK_BYTES = {Q4_K: 144, Q6_K: 210}
 
@@ -48,6 +49,12 @@ def lib():
         L.ns_last_error.restype = ctypes.c_char_p
         L.ns_layer_seed.restype = u64
         L.ns_layer_seed.argtypes = [u64, u32]
+        L.ns_nsmffn_fingerprint.restype = u64
+        L.ns_nsmffn_fingerprint.argtypes = [vp, u64, u64]
+        L.ns_nsmffn_data.restype = vp
+        L.ns_nsmffn_data.argtypes = [vp]
+        L.ns_nsmffn_size.restype = u64
+        L.ns_nsmffn_size.argtypes = [vp]
         sigs = {
             "ns_abi_version": [],
             "ns_ctx_create": [i32, ctypes.POINTER(vp)],
@@ -62,6 +69,11 @@ def lib():
             "ns_synth_blocks": [i32, u64, u64, u64, vp, i32],
             "ns_synth_normal_f32": [u64, u64, u64, vp, i32],
             "ns_synth_normal_f16": [u64, u64, u64, vp, i32],
+            "ns_nsmffn_convert": [ctypes.c_char_p, vp, u64, u64, vp, u32],
+            "ns_nsmffn_convert_in_place": [ctypes.c_char_p, ctypes.c_char_p, u64, vp, u32],
+            "ns_nsmffn_open": [ctypes.c_char_p, u64, u64, vp, u32, ctypes.POINTER(vp)],
+            "ns_nsmffn_close": [vp],
+            "ns_nsmffn_lookup": [vp, u64, ctypes.POINTER(u64), ctypes.POINTER(i32)],
         }
         for name, args in sigs.items():
             f = getattr(L, name)
@@ -130,6 +142,66 @@ def retile(src, qtype, cols, rows, from_layout, to_layout):
     dst = np.empty_like(src)
     check(lib().ns_retile(_ptr(src), _ptr(dst), qtype, cols, rows, from_layout, to_layout))
     return dst
+
+
+# ---- .nsmffn v3 files ---------------------------------------------------------
+
+TENSOR_DESC = np.dtype([("source_offset", "<u8"), ("bytes", "<u8"), ("type", "<u4"), ("cols", "<u4"),
+                        ("rows", "<u4"), ("layer", "<u4"), ("kind", "<u4"), ("reserved", "<u4")])
+assert TENSOR_DESC.itemsize == 40
+
+
+def tensor_table(rows):
+    """ns_tensor_desc array from (source_offset, bytes, type, cols, rows, layer, kind) tuples."""
+    return np.array([tuple(r) + (0,) for r in rows], dtype=TENSOR_DESC)
+
+
+def nsmffn_fingerprint(head, gguf_size):
+    head = np.ascontiguousarray(head, dtype=np.uint8)
+    return lib().ns_nsmffn_fingerprint(_ptr(head), head.size, gguf_size)
+
+
+def nsmffn_convert(path, gguf, data_offset, table):
+    gguf = np.ascontiguousarray(gguf, dtype=np.uint8)
+    check(lib().ns_nsmffn_convert(str(path).encode(), _ptr(gguf), gguf.size, data_offset, _ptr(table), len(table)))
+
+
+def nsmffn_convert_in_place(model_path, metadata_path, data_offset, table):
+    check(lib().ns_nsmffn_convert_in_place(str(model_path).encode(), str(metadata_path).encode(), data_offset,
+                                           _ptr(table), len(table)))
+
+
+class NsmffnFile:
+    """MetalFfnFile (src/native/metal_ffn.cpp:253-311): a validated read-only mapping."""
+
+    handle = None
+
+    def __init__(self, path, gguf_size, fingerprint, table):
+        h = ctypes.c_void_p()
+        check(lib().ns_nsmffn_open(str(path).encode(), gguf_size, fingerprint, _ptr(table), len(table),
+                                   ctypes.byref(h)))
+        self.handle = h
+
+    def close(self):
+        if self.handle:
+            lib().ns_nsmffn_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
+
+    def size(self):
+        return lib().ns_nsmffn_size(self.handle)
+
+    def lookup(self, source_offset):
+        off, re = ctypes.c_uint64(), ctypes.c_int()
+        check(lib().ns_nsmffn_lookup(self.handle, source_offset, ctypes.byref(off), ctypes.byref(re)))
+        return off.value, bool(re.value)
+
+    def view(self, offset, nbytes):
+        """Bytes [offset, offset + nbytes) of the mapping (a copy)."""
+        base = lib().ns_nsmffn_data(self.handle)
+        return np.frombuffer((ctypes.c_uint8 * nbytes).from_address(base + offset), dtype=np.uint8).copy()
 
 
 # ---- device entry points (torch tensors) ------------------------------------
