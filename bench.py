@@ -1,21 +1,29 @@
 """Benchmark of the quantised FFN path on one MI355X.
 
-Headline (BASELINE.json metric, config 1): decode Q6_K GEMV HBM GB/s.  One step
-= the ffn_down GEMV (Q6_K 3840 x 15360, rotating over 16 distinct weight copies
-so the 256 MB Infinity Cache cannot serve it) followed by the lm-head GEMV
-(Q6_K 262144 x 3840), both batch 1, CDNA4 layout, inputs resident in HBM.
+Headline (BASELINE.json metric, config 1): decode Q6_K GEMV HBM GB/s.  One step =
+the ffn_down GEMV (Q6_K 3840 x 15360, rotating over 16 distinct weight copies so
+the 256 MB Infinity Cache cannot serve it) followed by the lm-head GEMV (Q6_K
+262144 x 3840), both batch 1, CDNA4 layout, inputs resident in HBM.
 value = algorithmic bytes (weights + x + y) per step / time per step.
 
-Also reported under "extra": config 0 (Q4_K GEMV), config 2 (decode FFN block
-over 48 distinct layers) and config 3 (prefill FFN block at batch 1024,
-tokens/s, both accumulation modes).
+Also reported under "extra":
+  config 0  Q4_K GEMV 15360 x 3840 (16 rotating copies);
+  config 2  decode FFN block (gate/up Q4_K + GeGLU, down Q6_K), 48 distinct layers;
+  config 3  prefill FFN block at batch 1024, both accumulation modes, tokens/s;
+  config 4  48-layer FFN stack (Q4_K_M mix), prefill at batch 1024 then 64 decode
+            steps each ending in the lm-head GEMV; the decode step also replayed
+            from a HIP graph.
 
-usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+                       [--only all|headline|lmhead|prefill|stack]
+  --only lmhead runs just the lm-head GEMV (K launches) and a 256 MiB device copy
+  of known size: the driver for the rocprofv3 --pmc traffic runs.
 """
 import argparse
 import json
 import os
 import platform
+import re
 import sys
 import time
 
@@ -27,14 +35,32 @@ import numpy as np  # noqa: E402
 METRIC = "Q4_K/Q6_K GEMV HBM GB/s (decode); FFN prefill tokens/s @ batch 1024"
 HBM_PEAK_GBS = 8000.0
 FP16_MFMA_PEAK_TFLOPS = 2500.0
-D, F, V = 3840, 15360, 262144
+D, F, V, B = 3840, 15360, 262144, 1024
+NLAYERS, DECODE_STEPS = 48, 64
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic_lm_head_gemv.md")
 
-# algorithmic bytes (weights + fp32 x + fp32 y), SURVEY 8(d) per-unit figures
-BYTES_Q4_GATE = 15360 * 15 * 144 + 3840 * 4 + 15360 * 4          # 33,254,400
-BYTES_Q6_DOWN = 3840 * 60 * 210 + 15360 * 4 + 3840 * 4            # 48,460,800
-BYTES_Q6_LMHEAD = 262144 * 15 * 210 + 3840 * 4 + 262144 * 4       # 826,817,536
-BYTES_FFN_LAYER = 2 * 15360 * 15 * 144 + 3840 * 60 * 210         # 114,739,200 (weights)
-FLOPS_PREFILL_LAYER = 2 * 1024 * 15360 * 3840 * 2 + 2 * 1024 * 3840 * 15360  # 362,387,865,600
+
+def qbytes(qtype, rows, cols):
+    return rows * (cols // 256) * (144 if qtype == 12 else 210)
+
+
+Q4, Q6 = 12, 14
+# algorithmic bytes (weights + fp32 x + fp32 y) and flops per unit of work
+BYTES_Q4_GATE = qbytes(Q4, F, D) + 4 * D + 4 * F                 # 33,254,400
+BYTES_Q6_DOWN = qbytes(Q6, D, F) + 4 * F + 4 * D                 # 48,460,800
+BYTES_Q6_LMHEAD = qbytes(Q6, V, D) + 4 * D + 4 * V               # 826,817,536
+BYTES_FFN_LAYER = 2 * qbytes(Q4, F, D) + qbytes(Q6, D, F)        # 114,739,200 (weights)
+FLOPS_PREFILL_LAYER = 2 * B * F * D * 2 + 2 * B * D * F          # 362,387,865,600
+
+
+def down_type(layer):
+    """Config 4's Q4_K_M mix: ffn_down is Q6_K on even layers, Q4_K on odd layers (build's choice)."""
+    return Q6 if layer % 2 == 0 else Q4
+
+
+def is_global(layer):
+    """Gemma's 5 local : 1 global pattern: layer l is global (FP32 mode) when l % 6 == 5 (build's choice)."""
+    return layer % 6 == 5
 
 
 def log(*a):
@@ -51,188 +77,334 @@ def cpu_model():
     return platform.processor()
 
 
+def measured_traffic():
+    """HBM bytes per lm-head launch from the committed rocprofv3 --pmc summary, or None."""
+    try:
+        m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", open(TRAFFIC_FILE).read())
+        return int(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
+class Bench:
+    def __init__(self, args):
+        import torch
+        import nsffn as N
+
+        self.torch, self.N, self.args = torch, N, args
+        assert torch.cuda.is_available(), "no GPU visible"
+        torch.cuda.set_device(0)
+        self.ctx = N.Context(0)
+        self.stream = torch.cuda.current_stream()
+        self.extra = {}
+        self._stage = None
+
+    # -- inputs ---------------------------------------------------------------
+    def weights(self, qtype, seed, rows, cols):
+        """Seeded weights in the CDNA4 layout on the device (re-tiled on the device)."""
+        N, torch = self.N, self.torch
+        src = torch.from_numpy(N.synth_weights(qtype, seed, rows, cols)).cuda()
+        dst = torch.empty_like(src)
+        N.retile_device(src, dst, qtype, cols, rows, N.ROW_MAJOR, N.CDNA4)
+        return dst
+
+    def f32(self, seed, n):
+        return self.torch.from_numpy(self.N.synth_normal_f32(seed, n)).cuda()
+
+    def f16(self, seed, n):
+        return self.torch.from_numpy(self.N.synth_normal_f16(seed, n).view(np.int16)).cuda()
+
+    def timed(self, fn, n, warm=3):
+        torch = self.torch
+        for i in range(warm):
+            fn(i)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(self.stream)
+        for i in range(n):
+            fn(i)
+        b.record(self.stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n  # ms
+
+    # -- config 1 (headline) -----------------------------------------------------
+    def config1(self):
+        N, torch, args = self.N, self.torch, self.args
+        t0 = time.perf_counter()
+        self.lm_host = N.synth_weights(Q6, 0x1B, V, D)
+        self.lm = torch.from_numpy(N.retile(self.lm_host, Q6, D, V, N.ROW_MAJOR, N.CDNA4)).cuda()
+        self.down_host0 = N.synth_weights(Q6, 0xD0, D, F)
+        self.downs = [self.weights(Q6, 0xD0 + i, D, F) for i in range(16)]
+        self.x_lm_h, self.x_dn_h = N.synth_normal_f32(0x71, D), N.synth_normal_f32(0x72, F)
+        self.x_lm, self.x_dn = torch.from_numpy(self.x_lm_h).cuda(), torch.from_numpy(self.x_dn_h).cuda()
+        self.y_lm = torch.empty(V, dtype=torch.float32, device="cuda")
+        self.y_dn = torch.empty(D, dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        log(f"config1 inputs ready in {time.perf_counter() - t0:.1f}s")
+
+        ctx = self.ctx
+
+        def step(i, ev=None):
+            ctx.matmul(self.downs[i % 16], Q6, N.CDNA4, F, D, 1, self.x_dn, self.y_dn)
+            if ev is not None:
+                ev[0].record(self.stream)
+            ctx.matmul(self.lm, Q6, N.CDNA4, D, V, 1, self.x_lm, self.y_lm)
+            if ev is not None:
+                ev[1].record(self.stream)
+
+        for i in range(args.warmup):
+            step(i)
+        torch.cuda.synchronize()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            step(i, evs[i])
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        self.ms_per_step = 1e3 * wall / args.steps
+        self.value = (BYTES_Q6_DOWN + BYTES_Q6_LMHEAD) / (wall / args.steps) / 1e9
+        lm_ms = float(np.mean([a.elapsed_time(b) for a, b in evs]))
+        self.lm_gbs = BYTES_Q6_LMHEAD / (lm_ms * 1e-3) / 1e9
+        log(f"config1: {self.ms_per_step:.4f} ms/step, {self.value:.1f} GB/s; lm-head {lm_ms * 1e3:.1f} us "
+            f"= {self.lm_gbs:.1f} GB/s")
+        self.extra.update(lm_head_us=round(lm_ms * 1e3, 2), lm_head_GBps=round(self.lm_gbs, 1))
+        dn_ms = self.timed(lambda i: ctx.matmul(self.downs[i % 16], Q6, N.CDNA4, F, D, 1, self.x_dn, self.y_dn), 64)
+        self.extra.update(cfg1a_down_us=round(dn_ms * 1e3, 2),
+                          cfg1a_down_GBps=round(BYTES_Q6_DOWN / (dn_ms * 1e-3) / 1e9, 1))
+
+    def cpu_baseline(self):
+        """The oracle (dequant-once, sequential fp32 dot per row, threaded over rows) on whole
+        config-1 steps for about 10 s; also a parity check of the GPU on the same inputs."""
+        N = self.N
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import ns_oracle as O
+
+        nthreads = N.default_threads()
+        reps, t = 0, time.perf_counter()
+        while True:
+            ref_dn = O.gemv(Q6, O.ROW_MAJOR, self.down_host0, F, D, self.x_dn_h, nthreads=nthreads)
+            ref_lm = O.gemv(Q6, O.ROW_MAJOR, self.lm_host, D, V, self.x_lm_h, nthreads=nthreads)
+            reps += 1
+            dt = time.perf_counter() - t
+            if dt >= 10.0 or reps >= 200:
+                break
+        step_bytes = BYTES_Q6_DOWN + BYTES_Q6_LMHEAD
+        cpu = {"value": round(reps * step_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
+               "sample": f"{reps} full config-1 steps (Q6_K down 3840x15360 + lm-head 262144x3840 GEMV) by the "
+                         f"oracle's dequant-once sequential-fp32 dot, {dt:.2f} s on {cpu_model()}"}
+        self.ctx.matmul(self.downs[0], Q6, N.CDNA4, F, D, 1, self.x_dn, self.y_dn)
+        self.ctx.matmul(self.lm, Q6, N.CDNA4, D, V, 1, self.x_lm, self.y_lm)
+        self.torch.cuda.synchronize()
+
+        def rel(a, b):
+            return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
+        self.extra["parity_rel_err_down"] = rel(self.y_dn.cpu().numpy(), ref_dn)
+        self.extra["parity_rel_err_lm_head"] = rel(self.y_lm.cpu().numpy(), ref_lm)
+        log(f"cpu baseline {cpu['value']} GB/s in {dt:.2f}s; parity {self.extra['parity_rel_err_down']:.2e} "
+            f"{self.extra['parity_rel_err_lm_head']:.2e}")
+        return cpu
+
+    # -- config 0 and 3 ------------------------------------------------------------
+    def config0(self):
+        N, torch, ctx = self.N, self.torch, self.ctx
+        gates = [self.weights(Q4, 0x60 + i, F, D) for i in range(16)]
+        x = self.f32(0x61, D)
+        y = torch.empty(F, dtype=torch.float32, device="cuda")
+        ms = self.timed(lambda i: ctx.matmul(gates[i % 16], Q4, N.CDNA4, D, F, 1, x, y), 64)
+        self.extra.update(cfg0_q4k_gemv_us=round(ms * 1e3, 2),
+                          cfg0_q4k_gemv_GBps=round(BYTES_Q4_GATE / (ms * 1e-3) / 1e9, 1))
+        log(f"config0: {ms * 1e3:.2f} us = {BYTES_Q4_GATE / (ms * 1e-3) / 1e9:.1f} GB/s")
+
+    def config3(self):
+        N, torch, ctx = self.N, self.torch, self.ctx
+        g = [self.weights(Q4, 0x90 + i, F, D) for i in range(2)]
+        u = [self.weights(Q4, 0x92 + i, F, D) for i in range(2)]
+        dn = [self.weights(Q6, 0x94 + i, D, F) for i in range(2)]
+        xp = self.f16(0x96, B * D)
+        hp = torch.empty((B, F), dtype=torch.int16, device="cuda")
+        yp = torch.empty((B, D), dtype=torch.float32, device="cuda")
+        for fast, name in ((False, "fp32acc"), (True, "fp16acc")):
+            def block(i, fast=fast):
+                ctx.gate_up_geglu_rm32(g[i % 2], u[i % 2], N.CDNA4, D, F, B, xp, hp, fast)
+                ctx.ffn_down(dn[i % 2], Q6, N.CDNA4, F, D, B, hp, yp, True, fast)
+            p_ms = self.timed(block, 8, warm=2)
+            gu_ms = self.timed(lambda i, fast=fast: ctx.gate_up_geglu_rm32(g[i % 2], u[i % 2], N.CDNA4, D, F, B,
+                                                                           xp, hp, fast), 8, warm=1)
+            dn_ms = self.timed(lambda i, fast=fast: ctx.ffn_down(dn[i % 2], Q6, N.CDNA4, F, D, B, hp, yp, True,
+                                                                 fast), 8, warm=1)
+            tf = FLOPS_PREFILL_LAYER / (p_ms * 1e-3) / 1e12
+            self.extra.update({f"cfg3_prefill_{name}_tokens_per_s": round(B / (p_ms * 1e-3), 1),
+                               f"cfg3_prefill_{name}_block_ms": round(p_ms, 4),
+                               f"cfg3_prefill_{name}_TFLOPs": round(tf, 1),
+                               f"cfg3_prefill_{name}_mfma_frac": round(tf / FP16_MFMA_PEAK_TFLOPS, 4),
+                               f"cfg3_{name}_gate_up_ms": round(gu_ms, 4), f"cfg3_{name}_down_ms": round(dn_ms, 4)})
+            log(f"config3 {name}: {p_ms:.3f} ms/block = {B / (p_ms * 1e-3):.0f} tok/s, {tf:.0f} TFLOP/s "
+                f"(gate/up {gu_ms:.3f} ms, down {dn_ms:.3f} ms)")
+
+    # -- configs 2 and 4: the 48-layer stack -------------------------------------------
+    def stack(self):
+        N, torch, ctx = self.N, self.torch, self.ctx
+        t0 = time.perf_counter()
+        layers = []
+        for l in range(NLAYERS):
+            s = N.layer_seed(0xC4, l)
+            lay = {"gate": self.weights(Q4, s + 1, F, D), "up": self.weights(Q4, s + 2, F, D),
+                   "down6": self.weights(Q6, s + 3, D, F)}
+            lay["down"] = lay["down6"] if down_type(l) == Q6 else self.weights(Q4, s + 4, D, F)
+            layers.append(lay)
+        if not hasattr(self, "lm"):
+            self.lm = self.weights(Q6, 0x1B, V, D)
+        torch.cuda.synchronize()
+        log(f"stack weights ready in {time.perf_counter() - t0:.1f}s")
+
+        # ---- config 2: decode FFN block (Q6_K down) over 48 distinct layers -------------
+        x = self.f32(0x21, D)
+        h = torch.empty(F, dtype=torch.float32, device="cuda")
+        y = torch.empty(D, dtype=torch.float32, device="cuda")
+        xs = torch.empty(D, dtype=torch.float32, device="cuda")
+
+        def blocks(_i=0):
+            inp = x
+            for lay in layers:
+                ctx.ffn_block(lay["gate"], lay["up"], lay["down6"], Q6, N.CDNA4, D, F, 1, inp, h, y, False, True)
+                ctx.standardize(y, 1, D, xs, False)
+                inp = xs
+        ms = self.timed(blocks, 4, warm=1) / NLAYERS
+        self.extra.update(cfg2_ffn_block_decode_us=round(ms * 1e3, 2),
+                          cfg2_ffn_block_decode_GBps=round(BYTES_FFN_LAYER / (ms * 1e-3) / 1e9, 1))
+        log(f"config2: {ms * 1e3:.2f} us per decode FFN block = {BYTES_FFN_LAYER / (ms * 1e-3) / 1e9:.1f} GB/s")
+
+        # ---- config 4: prefill 1024 tokens through 48 layers, then 64 decode steps -------
+        xp = self.f16(0x41, B * D)
+        hp = torch.empty((B, F), dtype=torch.int16, device="cuda")
+        yp = torch.empty((B, D), dtype=torch.float32, device="cuda")
+        xq = torch.empty((B, D), dtype=torch.int16, device="cuda")
+
+        def prefill(_i=0):
+            inp = xp
+            for l, lay in enumerate(layers):
+                ctx.ffn_block(lay["gate"], lay["up"], lay["down"], down_type(l), N.CDNA4, D, F, B, inp, hp, yp,
+                              True, not is_global(l))
+                ctx.standardize(yp, B, D, xq, True)
+                inp = xq
+        p_ms = self.timed(prefill, 3, warm=1)
+        flops = NLAYERS * FLOPS_PREFILL_LAYER
+        self.extra.update(cfg4_prefill_ms=round(p_ms, 3), cfg4_prefill_tokens_per_s=round(B / (p_ms * 1e-3), 1),
+                          cfg4_prefill_TFLOPs=round(flops / (p_ms * 1e-3) / 1e12, 1))
+        log(f"config4 prefill: {p_ms:.2f} ms for {NLAYERS} layers = {B / (p_ms * 1e-3):.0f} tok/s")
+
+        xd = torch.empty(D, dtype=torch.float32, device="cuda")
+        xd.copy_(self.f32(0x42, D))
+        logits = torch.empty(V, dtype=torch.float32, device="cuda")
+
+        def decode_step(_i=0):
+            inp = xd
+            for l, lay in enumerate(layers):
+                ctx.ffn_block(lay["gate"], lay["up"], lay["down"], down_type(l), N.CDNA4, D, F, 1, inp, h, y,
+                              False, not is_global(l))
+                ctx.standardize(y, 1, D, xs, False)
+                inp = xs
+            ctx.matmul(self.lm, Q6, N.CDNA4, D, V, 1, xs, logits)
+            xd.copy_(xs)  # the next step starts from this step's final hidden state
+
+        step_bytes = sum(2 * qbytes(Q4, F, D) + qbytes(down_type(l), D, F) for l in range(NLAYERS)) + \
+            qbytes(Q6, V, D)
+        xd0 = xd.clone()
+        d_ms = self.timed(decode_step, DECODE_STEPS, warm=1)
+        # the same 64 steps replayed from one captured HIP graph of a decode step
+        xd.copy_(xd0)
+        decode_step()
+        torch.cuda.synchronize()
+        eager_logits = logits.clone()
+        graph = torch.cuda.CUDAGraph()
+        xd.copy_(xd0)
+        with torch.cuda.graph(graph):
+            decode_step()
+        xd.copy_(xd0)
+        graph.replay()
+        torch.cuda.synchronize()
+        replay_equal = bool(torch.equal(eager_logits, logits))
+        g_ms = self.timed(lambda i: graph.replay(), DECODE_STEPS, warm=2)
+        self.extra.update(cfg4_decode_ms_per_step=round(d_ms, 4), cfg4_decode_graph_ms_per_step=round(g_ms, 4),
+                          cfg4_decode_step_bytes=step_bytes,
+                          cfg4_decode_graph_GBps=round(step_bytes / (g_ms * 1e-3) / 1e9, 1),
+                          cfg4_graph_replay_bit_exact=replay_equal)
+        log(f"config4 decode: {d_ms:.3f} ms/step eager, {g_ms:.3f} ms/step graph = "
+            f"{step_bytes / (g_ms * 1e-3) / 1e9:.1f} GB/s; graph replay == eager: {replay_equal}")
+
+    # -- PMC driver -----------------------------------------------------------------------
+    def lmhead_only(self):
+        N, torch, ctx = self.N, self.torch, self.ctx
+        lm = self.weights(Q6, 0x1B, V, D)
+        x = self.f32(0x71, D)
+        y = torch.empty(V, dtype=torch.float32, device="cuda")
+        a = torch.ones(64 << 20, dtype=torch.float32, device="cuda")  # 256 MiB, the copy of known size
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        for _ in range(self.args.steps):
+            ctx.matmul(lm, Q6, N.CDNA4, D, V, 1, x, y)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log(f"lm-head GEMV x{self.args.steps} and 3 x 256 MiB device copies done")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--quick", action="store_true", help="headline only (no extra configs)")
+    ap.add_argument("--quick", action="store_true", help="same as --only headline")
+    ap.add_argument("--only", default="all", choices=["all", "headline", "lmhead", "prefill", "stack"])
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (asked for {args.gpus}); the multi-GPU design is "
-              "described in DESIGN.md and is not run.", file=sys.stderr)
+        print(f"bench.py measures one GPU only (asked for {args.gpus}); how the path would shard is described "
+              "in DESIGN.md and is not run.", file=sys.stderr)
         sys.exit(2)
-
-    import torch
-    import nsffn as N
-
-    assert torch.cuda.is_available(), "no GPU visible"
-    torch.cuda.set_device(0)
-    ctx = N.Context(0)
-    stream = torch.cuda.current_stream()
-    nthreads = N.default_threads()
-
-    def upload(host, qtype, cols, rows):
-        return torch.from_numpy(N.retile(host, qtype, cols, rows, N.ROW_MAJOR, N.CDNA4)).cuda()
-
-    # ---- config 1 inputs -------------------------------------------------------
-    t_gen = time.perf_counter()
-    lm_host = N.synth_weights(N.Q6_K, 0x1B, V, D)
-    lm = upload(lm_host, N.Q6_K, D, V)
-    down_host0 = N.synth_weights(N.Q6_K, 0xD0, D, F)
-    downs = [upload(down_host0, N.Q6_K, F, D)]
-    for i in range(1, 16):
-        downs.append(upload(N.synth_weights(N.Q6_K, 0xD0 + i, D, F), N.Q6_K, F, D))
-    x_lm_h = N.synth_normal_f32(0x71, D)
-    x_dn_h = N.synth_normal_f32(0x72, F)
-    x_lm, x_dn = torch.from_numpy(x_lm_h).cuda(), torch.from_numpy(x_dn_h).cuda()
-    y_lm = torch.empty(V, dtype=torch.float32, device="cuda")
-    y_dn = torch.empty(D, dtype=torch.float32, device="cuda")
-    torch.cuda.synchronize()
-    log(f"inputs ready in {time.perf_counter() - t_gen:.1f}s")
-
-    def step(i, ev=None):
-        ctx.matmul(downs[i % 16], N.Q6_K, N.CDNA4, F, D, 1, x_dn, y_dn)
-        if ev is not None:
-            ev[0].record(stream)
-        ctx.matmul(lm, N.Q6_K, N.CDNA4, D, V, 1, x_lm, y_lm)
-        if ev is not None:
-            ev[1].record(stream)
-
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i, evs[i])
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    wall = t1 - t0
-    ms_per_step = 1e3 * wall / args.steps
-    bytes_step = BYTES_Q6_DOWN + BYTES_Q6_LMHEAD
-    value = bytes_step / (wall / args.steps) / 1e9
-    lm_ms = float(np.mean([a.elapsed_time(b) for a, b in evs]))
-    lm_gbs = BYTES_Q6_LMHEAD / (lm_ms * 1e-3) / 1e9
-    log(f"config1: {ms_per_step:.4f} ms/step, {value:.1f} GB/s; lm-head {lm_ms * 1e3:.1f} us = {lm_gbs:.1f} GB/s")
-
-    extra = {"lm_head_us": round(lm_ms * 1e3, 2), "lm_head_GBps": round(lm_gbs, 1)}
-
-    def timed(fn, n, warm=3):
-        for i in range(warm):
-            fn(i)
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for i in range(n):
-            fn(i)
-        b.record(stream)
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / n  # ms
-
-    # down GEMV alone (rotating copies)
-    dn_ms = timed(lambda i: ctx.matmul(downs[i % 16], N.Q6_K, N.CDNA4, F, D, 1, x_dn, y_dn), 64)
-    extra["cfg1a_down_us"] = round(dn_ms * 1e3, 2)
-    extra["cfg1a_down_GBps"] = round(BYTES_Q6_DOWN / (dn_ms * 1e-3) / 1e9, 1)
-
-    if not args.quick:
-        # ---- config 0: Q4_K GEMV 15360 x 3840, 16 rotating copies -------------
-        gates = [upload(N.synth_weights(N.Q4_K, 0x60 + i, F, D), N.Q4_K, D, F) for i in range(16)]
-        y_g = torch.empty(F, dtype=torch.float32, device="cuda")
-        g_ms = timed(lambda i: ctx.matmul(gates[i % 16], N.Q4_K, N.CDNA4, D, F, 1, x_lm, y_g), 64)
-        extra["cfg0_q4k_gemv_us"] = round(g_ms * 1e3, 2)
-        extra["cfg0_q4k_gemv_GBps"] = round(BYTES_Q4_GATE / (g_ms * 1e-3) / 1e9, 1)
-        # ---- config 2: decode FFN block, 16 distinct layers in rotation -------
-        ups = [upload(N.synth_weights(N.Q4_K, 0x80 + i, F, D), N.Q4_K, D, F) for i in range(16)]
-        h_d = torch.empty(F, dtype=torch.float32, device="cuda")
-
-        def block(i):
-            ctx.gate_up_geglu_decode(gates[i % 16], ups[i % 16], N.CDNA4, D, F, x_lm, h_d)
-            ctx.matmul(downs[i % 16], N.Q6_K, N.CDNA4, F, D, 1, h_d, y_dn)
-
-        b_ms = timed(block, 48)
-        extra["cfg2_ffn_block_decode_us"] = round(b_ms * 1e3, 2)
-        extra["cfg2_ffn_block_decode_GBps"] = round(BYTES_FFN_LAYER / (b_ms * 1e-3) / 1e9, 1)
-        del ups
-        # ---- config 3: prefill FFN block at batch 1024 --------------------------
-        B = 1024
-        xp = torch.from_numpy(N.synth_normal_f16(0x90, B * D).view(np.int16)).cuda()
-        hp = torch.empty((B, F), dtype=torch.int16, device="cuda")
-        yp = torch.empty((B, D), dtype=torch.float32, device="cuda")
-        for fast, name in ((False, "fp32acc"), (True, "fp16acc")):
-            def pre(i, fast=fast):
-                ctx.gate_up_geglu_rm32(gates[i % 16], gates[(i + 1) % 16], N.CDNA4, D, F, B, xp, hp, fast)
-                ctx.ffn_down(downs[i % 16], N.Q6_K, N.CDNA4, F, D, B, hp, yp, True, fast)
-            p_ms = timed(pre, 8, warm=2)
-            gu_ms = timed(lambda i, fast=fast: ctx.gate_up_geglu_rm32(gates[i % 16], gates[(i + 1) % 16], N.CDNA4,
-                                                                      D, F, B, xp, hp, fast), 8, warm=1)
-            dn2_ms = timed(lambda i, fast=fast: ctx.ffn_down(downs[i % 16], N.Q6_K, N.CDNA4, F, D, B, hp, yp, True,
-                                                             fast), 8, warm=1)
-            extra[f"cfg3_prefill_{name}_tokens_per_s"] = round(B / (p_ms * 1e-3), 1)
-            extra[f"cfg3_prefill_{name}_block_ms"] = round(p_ms, 4)
-            extra[f"cfg3_prefill_{name}_TFLOPs"] = round(FLOPS_PREFILL_LAYER / (p_ms * 1e-3) / 1e12, 1)
-            extra[f"cfg3_{name}_gate_up_ms"] = round(gu_ms, 4)
-            extra[f"cfg3_{name}_down_ms"] = round(dn2_ms, 4)
-            log(f"config3 {name}: {p_ms:.3f} ms/block = {B / (p_ms * 1e-3):.0f} tok/s "
-                f"(gate/up {gu_ms:.3f} ms, down {dn2_ms:.3f} ms)")
-        del gates
-
-    # ---- CPU baseline: the oracle on one full config-1 step --------------------
-    cpu = None
-    if not args.no_cpu:
-        sys.path.insert(0, os.path.join(ROOT, "oracle"))
-        import ns_oracle as O
-
-        # repeat whole config-1 steps until at least 10 s of CPU time have passed
-        reps = 0
-        t = time.perf_counter()
-        while True:
-            ref_dn = O.gemv(N.Q6_K, O.ROW_MAJOR, down_host0, F, D, x_dn_h, nthreads=nthreads)
-            ref_lm = O.gemv(N.Q6_K, O.ROW_MAJOR, lm_host, D, V, x_lm_h, nthreads=nthreads)
-            reps += 1
-            dt = time.perf_counter() - t
-            if dt >= 10.0 or reps >= 200:
-                break
-        cpu = {"value": round(reps * bytes_step / dt / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
-               "sample": f"{reps} full config-1 steps (Q6_K down 3840x15360 + lm-head 262144x3840 GEMV) by the "
-                         f"oracle's dequant-once sequential-fp32 dot, {dt:.2f} s on {cpu_model()}"}
-        # the same inputs on the GPU: a free parity check of the measured kernels
-        ctx.matmul(downs[0], N.Q6_K, N.CDNA4, F, D, 1, x_dn, y_dn)
-        ctx.matmul(lm, N.Q6_K, N.CDNA4, D, V, 1, x_lm, y_lm)
-        torch.cuda.synchronize()
-
-        def rel(a, b):
-            return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
-        extra["parity_rel_err_down"] = rel(y_dn.cpu().numpy(), ref_dn)
-        extra["parity_rel_err_lm_head"] = rel(y_lm.cpu().numpy(), ref_lm)
-        log(f"cpu baseline {cpu['value']} GB/s in {dt:.2f}s; parity {extra['parity_rel_err_down']:.2e} "
-            f"{extra['parity_rel_err_lm_head']:.2e}")
-
+    only = "headline" if args.quick else args.only
+    bench = Bench(args)
+    if only == "lmhead":
+        bench.lmhead_only()
+        return
+    if only == "prefill":
+        bench.config3()
+        print(json.dumps({"extra": bench.extra}), flush=True)
+        return
+    if only == "stack":
+        bench.stack()
+        print(json.dumps({"extra": bench.extra}), flush=True)
+        return
+    bench.config1()
+    if only == "all":
+        bench.config0()
+        bench.config3()
+        bench.stack()
+    cpu = None if args.no_cpu else bench.cpu_baseline()
     out = {
         "metric": METRIC,
-        "value": round(value, 1),
+        "value": round(bench.value, 1),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": round(bench.ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded generator, BASELINE config 1 distributions)",
+        "data": "synthetic (seeded generator, BASELINE config distributions)",
         "config": {"workload": "config 1: Q6_K ffn_down 3840x15360 (16 rotating copies) + Q6_K lm-head "
                                "262144x3840 GEMV, batch 1, CDNA4 layout",
-                   "batch": 1, "bytes_per_step": bytes_step},
-        "roofline": {"bound": "hbm", "achieved": round(lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gemv_kernel<Q6_K, CDNA4> (lm-head)"},
+                   "batch": 1, "bytes_per_step": BYTES_Q6_DOWN + BYTES_Q6_LMHEAD},
+        "roofline": {"bound": "hbm", "achieved": round(bench.lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(bench.lm_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "kernel": "gemv_kernel<Q6_K, CDNA4> (lm-head, 826,817,536 algorithmic bytes per launch)"},
         "cpu_baseline": cpu,
-        "extra": extra,
+        "extra": bench.extra,
     }
     print(json.dumps(out), flush=True)
-    ctx.close()
+    bench.ctx.close()
 
 
 if __name__ == "__main__":

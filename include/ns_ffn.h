@@ -104,6 +104,16 @@ int ns_ffn_down(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols,
 int ns_dequant(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, uint32_t rows,
                uint32_t row0, uint32_t nrows, float *out_f32, uint16_t *out_f16, void *stream);
 
+/* Inter-layer step of BASELINE config 4 (the 48-layer FFN stack), which keeps the hidden
+ * state an N(0,1) vector at unit RMS: per token, out[t] = (y[t] - m) / sqrt(mean_k (y[t][k] - m)^2)
+ * with m = mean_k y[t][k], as fp16 bits (out_half != 0) or fp32; a constant row maps to zeros.
+ * The mean is removed because the synthetic weights have a positive mean that makes an uncentred
+ * chain collapse.  It takes the place of the engine's residual-add + RMSNorm between FFN blocks
+ * (rms_add_then_half, metal:523-529; mm:563, mm:574), which is outside this path.
+ * y fp32 [batch][cols]. */
+int ns_standardize(ns_ctx *ctx, const float *y, uint32_t batch, uint32_t cols, void *out, int out_half,
+                   void *stream);
+
 /* ---- host-side (CPU) utilities; no GPU needed ------------------------------ */
 
 /* Convert a host tensor between layouts (a14; the conversion step of

@@ -193,3 +193,11 @@ extern "C" int ns_retile_device(const void *src, void *dst, int type, uint32_t c
                                        rows, from_layout, to_layout, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? NS_OK : hip_fail(e, "ns_retile_device");
 }
+
+extern "C" int ns_standardize(ns_ctx *ctx, const float *y, uint32_t batch, uint32_t cols, void *out, int out_half,
+                              void *stream) {
+    if (!ctx) return fail(NS_ERR_ARG, "ns_standardize: null context");
+    if (!y || !out || batch == 0 || cols == 0) return fail(NS_ERR_ARG, "ns_standardize: null buffer or empty shape");
+    const hipError_t e = launch_standardize(y, batch, cols, out, out_half != 0, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? NS_OK : hip_fail(e, "ns_standardize");
+}

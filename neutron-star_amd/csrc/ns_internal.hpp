@@ -46,6 +46,9 @@ hipError_t launch_dequant(int type, int layout, const uint8_t *w, uint32_t cols,
                           uint32_t row0, uint32_t nrows, float *out_f32, uint16_t *out_f16,
                           hipStream_t stream);
 
+// x[t] = (y[t] - mean(y[t])) / rms(y[t] - mean(y[t])) per token, fp16 (half) or fp32 out.
+hipError_t launch_standardize(const float *y, uint32_t batch, uint32_t cols, void *out, bool half, hipStream_t stream);
+
 hipError_t launch_retile(int type, const uint8_t *src, uint8_t *dst, uint32_t cols,
                          uint32_t rows, int from_layout, int to_layout, hipStream_t stream);
 

@@ -138,6 +138,32 @@ public:
                           half_input ? 1 : 0, fast_swa ? 1 : 0, out, e));
     }
 
+    // The FFN part of the engine's per-layer loop (mm:564-573): gate/up + GeGLU
+    // into `mid`, then the down projection into `out`, in the accumulation mode
+    // fast_swa_ffn = prefill && swa && !exact_ffn (mm:565).  Prefill: `in` is fp16
+    // [batch][cols] (halfbuf) and `mid` fp16 [batch][ffn]; decode: both fp32.
+    void ffn_block(hipStream_t e, const Tensor &gate, const Tensor &up, const Tensor &down, const void *in, void *mid,
+                   float *out, uint32_t batch, bool prefill, bool swa, bool exact_ffn) const {
+        const bool fast_swa = prefill && swa && !exact_ffn;
+        if (prefill) {
+            gate_up_geglu_rm32(e, gate, up, static_cast<const uint16_t *>(in), static_cast<uint16_t *>(mid), batch,
+                               fast_swa);
+        } else {
+            // mm:570-571: the fused decode kernel; batches of fp32 tokens take it token by token
+            const uint32_t c = cols(gate), r = rows(gate);
+            for (uint32_t t = 0; t < batch; ++t)
+                gate_up_geglu_decode(e, gate, up, static_cast<const float *>(in) + size_t(t) * c,
+                                     static_cast<float *>(mid) + size_t(t) * r);
+        }
+        ffn_down(e, down, mid, out, batch, prefill, fast_swa);
+    }
+
+    // Inter-layer step of the FFN stack: out = (y - mean) / rms(y - mean) per
+    // token, fp16 (half_out) or fp32; y fp32 [batch][cols].
+    void standardize(hipStream_t e, const float *y, uint32_t batch, uint32_t cols, void *out, bool half_out) const {
+        check(ns_standardize(ctx_, y, batch, cols, out, half_out ? 1 : 0, e));
+    }
+
 private:
     static uint32_t cols(const Tensor &t) { return uint32_t(t.shape.at(0)); }
     static uint32_t rows(const Tensor &t) { return t.shape.size() > 1 ? uint32_t(t.shape[1]) : 1u; }

@@ -64,6 +64,7 @@ def lib():
             "ns_gate_up_geglu_rm32": [vp, vp, vp, i32, u32, u32, u32, vp, vp, i32, vp],
             "ns_ffn_down": [vp, vp, i32, i32, u32, u32, u32, vp, i32, i32, vp, vp],
             "ns_dequant": [vp, vp, i32, i32, u32, u32, u32, u32, vp, vp, vp],
+            "ns_standardize": [vp, vp, u32, u32, vp, i32, vp],
             "ns_retile": [vp, vp, i32, u32, u32, i32, i32],
             "ns_retile_device": [vp, vp, i32, u32, u32, i32, i32, vp],
             "ns_synth_blocks": [i32, u64, u64, u64, vp, i32],
@@ -238,6 +239,24 @@ class Context:
     def ffn_down(self, w, qtype, layout, cols, rows, batch, inp, out, half_input, fast_swa, stream=None):
         check(lib().ns_ffn_down(self.handle, _ptr(w), qtype, layout, cols, rows, batch, _ptr(inp),
                                 int(half_input), int(fast_swa), _ptr(out), _stream(stream)))
+
+    def ffn_block(self, gate, up, down, down_type, layout, cols, ffn, batch, inp, mid, out, prefill, swa,
+                  exact_ffn=False, stream=None):
+        """The FFN part of the engine's per-layer loop (metal_engine.mm:564-573): gate/up +
+        GeGLU into `mid`, then down into `out`, in the mode fast_swa_ffn = prefill && swa &&
+        !exact_ffn (mm:565).  Prefill: inp/mid fp16 bits; decode: fp32."""
+        fast = bool(prefill and swa and not exact_ffn)
+        if prefill:
+            self.gate_up_geglu_rm32(gate, up, layout, cols, ffn, batch, inp, mid, fast, stream)
+        else:
+            for t in range(batch):
+                self.gate_up_geglu_decode(gate, up, layout, cols, ffn, inp[t * cols:(t + 1) * cols] if batch > 1
+                                          else inp, mid[t * ffn:(t + 1) * ffn] if batch > 1 else mid, stream)
+        self.ffn_down(down, down_type, layout, ffn, cols, batch, mid, out, prefill, fast, stream)
+
+    def standardize(self, y, batch, cols, out, out_half, stream=None):
+        """Config 4's inter-layer step: out = (y - mean) / rms(y - mean) per token."""
+        check(lib().ns_standardize(self.handle, _ptr(y), batch, cols, _ptr(out), int(out_half), _stream(stream)))
 
     def dequant(self, w, qtype, layout, cols, rows, row0, nrows, out_f32=None, out_f16=None, stream=None):
         check(lib().ns_dequant(self.handle, _ptr(w), qtype, layout, cols, rows, row0, nrows,

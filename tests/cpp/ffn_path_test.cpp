@@ -2,7 +2,10 @@
 // the way the reference engine drives its FFN helpers (metal_engine.mm:562-576):
 // decode FFN block + lm-head, then a prefill FFN block in both accumulation
 // modes, each checked against the CPU oracle; then the error convention
-// (std::runtime_error).  Exit status 0 = pass.  Built by __graft_entry__.build()
+// (std::runtime_error); then the whole load chain of the engine: a GGUF image is
+// converted to .nsmffn (convert_metal_ffn), mapped and validated (MetalFfnFile),
+// uploaded with the CDNA4 re-tile (WeightImage), and run through ffn_block with
+// the per-layer accumulation-mode rule of mm:565.  Exit status 0 = pass.  Built by __graft_entry__.build()
 // and run by tests/test_gpu_cpp_path.py on the GPU.
 #include <cmath>
 #include <cstdio>
@@ -10,7 +13,10 @@
 #include <stdexcept>
 #include <vector>
 
+#include <unistd.h>
+
 #include "ffn_path.hpp"
+#include "nsmffn_file.hpp"
 #include "ns_oracle.h"
 
 using namespace neutron::amd;
@@ -145,6 +151,73 @@ int main() {
     threw = false;
     try { path.matmul(s, gate, dx, dh, 0); } catch (const std::runtime_error &e) { threw = std::strstr(e.what(), "batch") != nullptr; }
     expect(threw, "zero batch throws with the C ABI message");
+
+    // ---- load chain: GGUF image -> .nsmffn -> MetalFfnFile -> WeightImage -> ffn_block
+    {
+        const uint64_t data_offset = 65536 + 512;
+        const Tensor *ts[4] = {&gate, &up, &down, &embd};
+        const std::vector<uint8_t> *hs[4] = {&hg, &hu, &hd, &he};
+        std::vector<ns_tensor_desc> table;
+        uint64_t pos = 0;
+        for (int i = 0; i < 4; ++i) {
+            const Tensor &t = *ts[i];
+            const bool ffn = i < 3;
+            table.push_back({pos, t.bytes, uint32_t(t.type), uint32_t(t.shape[0]), uint32_t(t.shape[1]),
+                             ffn ? 0u : NS_FFN_NONE, ffn ? uint32_t(i) : NS_FFN_NONE, 0});
+            pos += (t.bytes + 31) / 32 * 32;
+        }
+        std::vector<uint8_t> gguf(data_offset + pos, 0);
+        for (size_t i = 0; i < data_offset; ++i) gguf[i] = uint8_t(i * 131 + 7);  // stand-in metadata bytes
+        for (int i = 0; i < 4; ++i)
+            std::memcpy(gguf.data() + data_offset + table[i].source_offset, hs[i]->data(), hs[i]->size());
+        const std::string file = "/tmp/ffn_path_test_" + std::to_string(getpid()) + ".nsmffn";
+        convert_metal_ffn(file, gguf.data(), gguf.size(), data_offset, table);
+        const uint64_t fp = metal_ffn_fingerprint(gguf.data(), data_offset, gguf.size());
+        MetalFfnFile mf(file, gguf.size(), fp, table);
+        expect(mf.reordered(table[0].source_offset) && !mf.reordered(table[3].source_offset),
+               "MetalFfnFile: FFN tensors reordered, embedding not");
+        // the engine's tensors are keyed by their GGUF offset
+        Tensor g2 = gate, u2 = up, d2 = down, e2 = embd;
+        Tensor *t2[4] = {&g2, &u2, &d2, &e2};
+        for (int i = 0; i < 4; ++i) t2[i]->offset = table[i].source_offset;
+        WeightImage img2;
+        img2.allocate(mf.file_size());
+        for (int i = 0; i < 4; ++i) {
+            const uint64_t o = mf.offset(t2[i]->offset);
+            img2.upload(*t2[i], mf.mapped_data() + o, o, mf.reordered(t2[i]->offset) ? Layout::Nsmffn : Layout::RowMajor,
+                        true, s);
+        }
+        FfnPath p2(img2);
+        // decode block (always FP32) + standardised rescale
+        float *dx2 = dev(std::vector<float>(D));
+        p2.ffn_block(s, g2, u2, d2, dx, dh, dy, 1, /*prefill=*/false, /*swa=*/true, /*exact_ffn=*/false);
+        p2.standardize(s, dy, 1, uint32_t(D), dx2, false);
+        if (hipStreamSynchronize(s) != hipSuccess) return 3;
+        const auto yb = host(dy, D), xr = host(dx2, D);
+        expect(rel_err(yb, y_ref, 1, D) <= 1e-3 && rel_err(host(dh, F), h_ref, 1, F) <= 1e-3,
+               "ffn_block decode from the .nsmffn file within 1e-3");
+        double ss = 0;
+        for (float v : xr) ss += double(v) * v;
+        expect(std::fabs(std::sqrt(ss / D) - 1.0) < 1e-5, "standardize output has unit RMS");
+        // prefill block: a local (swa) layer runs FP16 mode, a global one or --exact-ffn FP32 (mm:565)
+        for (int c = 0; c < 3; ++c) {
+            const bool swa = c != 1, exact = c == 2;
+            p2.ffn_block(s, g2, u2, d2, dxp, dhp, dyp, uint32_t(B), true, swa, exact);
+            if (hipStreamSynchronize(s) != hipSuccess) return 3;
+            const auto yq = host(dyp, B * D);
+            bool f16p = true;
+            for (float v : yq) {
+                uint32_t bits;
+                std::memcpy(&bits, &v, 4);
+                f16p = f16p && (bits & 0x1FFFu) == 0;
+            }
+            const bool fast = swa && !exact;
+            expect(f16p == fast, fast ? "local layer: FP16 mode (fp16-precision outputs)"
+                                      : "global layer / exact_ffn: FP32 mode (full-precision outputs)");
+        }
+        (void)hipFree(dx2);
+        std::remove(file.c_str());
+    }
 
     (void)hipFree(dx); (void)hipFree(dxe); (void)hipFree(dh); (void)hipFree(dy); (void)hipFree(dl);
     (void)hipFree(dxp); (void)hipFree(dhp); (void)hipFree(dyp);
