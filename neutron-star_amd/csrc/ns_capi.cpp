@@ -84,7 +84,7 @@ int gemm(ns_ctx *ctx, const char *fn, int type, int layout, int acc, const void 
     if (layout == ROW_MAJOR)
         return fail(NS_ERR_UNSUPPORTED, std::string(fn) + ": the prefill GEMM needs the NSMFFN or CDNA4 slab layout");
     size_t wf = 0, wc = 0;
-    gemm_workspace_need(type, cols, rows, batch, up != nullptr, &wf, &wc);
+    gemm_workspace_need(type, layout, cols, rows, batch, up != nullptr, &wf, &wc);
     if (int rc = ensure_ws(ctx, wf, wc)) return rc;
     const hipError_t e = launch_gemm(type, layout, acc, static_cast<const uint8_t *>(w),
                                      static_cast<const uint8_t *>(up), x, out, cols, rows, batch, ctx->ws, s);

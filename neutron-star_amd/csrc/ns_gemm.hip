@@ -616,8 +616,14 @@ static size_t xs_floats(int type, uint32_t cols, uint32_t batch) {
     return type == Q4_K ? ((size_t(batch) * (cols / 32) + 63) / 64) * 64 : 0;
 }
 
-void gemm_workspace_need(int type, uint32_t cols, uint32_t rows, uint32_t batch, bool pair, size_t *floats,
-                         size_t *counters) {
+void gemm_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, uint32_t batch, bool pair,
+                         size_t *floats, size_t *counters) {
+    if (layout == CDNA4 && type == Q4_K) {
+        size_t part = 0;
+        gemm_reg_workspace_need(cols, rows, batch, pair, &part, counters);
+        *floats = xs_floats(type, cols, batch) + part;
+        return;
+    }
     const GemmPlan p = plan_gemm(cols, rows, batch, pair);
     *floats = xs_floats(type, cols, batch) +
               (p.kparts > 1 ? size_t(p.kparts) * (pair ? 2 : 1) * batch * rows : 0);
@@ -636,6 +642,9 @@ hipError_t launch_gemm(int type, int layout, int acc, const uint8_t *w, const ui
         if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     }
     const size_t off = xs_floats(type, cols, batch);
+    // Q4_K on the CDNA4 layout: register-resident weight fragments (ns_gemm_reg.hip)
+    if (layout == CDNA4 && type == Q4_K)
+        return launch_gemm_reg(acc, w, up, x, xh, out, cols, rows, batch, ws.partial + off, ws.counters, stream);
     if (up) return launch_layout<Q4_K, true>(layout, acc, w, up, x, xh, out, cols, rows, batch, ws, off, stream);
     if (type == Q4_K)
         return launch_layout<Q4_K, false>(layout, acc, w, nullptr, x, xh, out, cols, rows, batch, ws, off, stream);

@@ -31,7 +31,12 @@
 namespace ns {
 namespace {
 
-constexpr uint32_t kWgWaves = 4;  // waves per workgroup
+constexpr uint32_t kWgWaves = 4;   // waves per workgroup of the flattened split
+
+// Largest workgroup (in waves) a kernel instance supports: as many as one CU
+// holds at that kernel's register use (Q4_K ~110 VGPRs: 4 per SIMD; Q6_K
+// ~160: 3; gate/up pair ~190: 2).
+constexpr uint32_t max_wg_waves(int type, bool pair) { return pair ? 8 : (type == Q4_K ? 16 : 12); }
 
 // ---- block loads --------------------------------------------------------
 
@@ -202,8 +207,9 @@ __device__ __forceinline__ void group_sums(const float *__restrict__ xb, uint32_
 
 // Flattened work: unit i = (slab i / nb, super-block i % nb), i < U = nslabs * nb.
 // Workgroup g of G takes units [first(g), first(g+1)) with first(g) = g*q +
-// min(g, r), q = U / G, r = U % G, and splits them evenly over its kWgWaves
-// waves, so every wave streams the same amount of weights.  A wave writes the
+// min(g, r), q = U / G, r = U % G, and splits them evenly over its waves, so
+// every wave streams the same amount of weights.  With G = nslabs every
+// workgroup owns one whole slab and no slab is cut between workgroups.  A wave writes the
 // slabs it covers whole.  Parts of slabs cut between waves meet in LDS (wave
 // order); a slab cut between workgroups is finished by the last of its
 // workgroups to arrive, which adds the workgroup parts in workgroup order.
@@ -219,20 +225,22 @@ struct Split {
 };
 
 template <int TYPE, int LAYOUT, bool PAIR>
-__global__ __launch_bounds__(kWgWaves * 64) void gemv_kernel(
+__global__ __launch_bounds__(max_wg_waves(TYPE, PAIR) * 64) void gemv_kernel(
     const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, const float *__restrict__ x,
     float *__restrict__ out, uint32_t rows, uint32_t nb, uint32_t nslabs, float *__restrict__ partial,
     uint32_t *__restrict__ counters) {
     constexpr uint32_t kPlanes = PAIR ? 2 : 1;
-    __shared__ float lds_part[kWgWaves][2][kPlanes][64];
-    __shared__ uint32_t lds_slab[kWgWaves][2];
+    constexpr uint32_t kMaxW = max_wg_waves(TYPE, PAIR);
+    __shared__ float lds_part[kMaxW][2][kPlanes][64];
+    __shared__ uint32_t lds_slab[kMaxW][2];
+    const uint32_t nw = blockDim.x >> 6;  // waves in this workgroup (<= kMaxW)
 
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t G = gridDim.x, g = blockIdx.x, U = nslabs * nb;
     const Split sp{U / G, U % G};
     const uint32_t wg0 = sp.first(g), wg1 = sp.first(g + 1), n = wg1 - wg0;
-    const uint32_t i0 = wg0 + wave * n / kWgWaves, i1 = wg0 + (wave + 1) * n / kWgWaves;
+    const uint32_t i0 = wg0 + wave * n / nw, i1 = wg0 + (wave + 1) * n / nw;
 
     if (lane < 2) lds_slab[wave][lane] = ~0u;
     float acc0 = 0.f, acc1 = 0.f;
@@ -323,10 +331,10 @@ __global__ __launch_bounds__(kWgWaves * 64) void gemv_kernel(
     // Slabs parked in LDS: at most the workgroup's first and last slab (cut
     // between workgroups) and slabs cut only between its own waves.
     __syncthreads();
-    for (uint32_t s = s_lo + wave; s <= s_hi; s += kWgWaves) {
+    for (uint32_t s = s_lo + wave; s <= s_hi; s += nw) {
         float r0 = 0.f, r1 = 0.f;
         bool any = false;
-        for (uint32_t v = 0; v < kWgWaves; ++v)
+        for (uint32_t v = 0; v < nw; ++v)
 #pragma unroll
             for (uint32_t k = 0; k < 2; ++k)
                 if (lds_slab[v][k] == s) {
@@ -428,20 +436,30 @@ int waves_per_cu() {
 }
 
 struct GemvPlan {
-    uint32_t nslabs, G;  // G workgroups of kWgWaves waves
+    uint32_t nslabs, G, W;  // G workgroups of W waves
 };
 
 // G: as many workgroups as the device holds at once (never more than there
 // are units).  Measured on MI355X this is at or near the best grid for every
 // shape of the path: the 262144-row lm-head (4096 slabs, 1.3 slabs per wave),
 // the 3840-row down projection and the 15360-row gate/up projections.
-GemvPlan plan_gemv(uint32_t cols, uint32_t rows, int resident_waves) {
+GemvPlan plan_gemv(uint32_t cols, uint32_t rows, int resident_waves, uint32_t max_waves, uint32_t cus) {
     GemvPlan p;
     const uint32_t nb = cols / kQK;
     p.nslabs = (rows + kRowTile - 1) / kRowTile;
     const uint32_t U = p.nslabs * nb;
     uint32_t cap = uint32_t(resident_waves > 0 ? resident_waves : 2048);
     if (const int e = env_int("NS_GEMV_WAVES", 0); e > 0) cap = uint32_t(e);
+    // About one slab per CU (the 15360-row gate/up projections: 240 slabs): one
+    // workgroup per slab, as many waves as the CU holds -- nothing crosses
+    // workgroups.  Otherwise the flattened split over resident 4-wave workgroups.
+    const bool whole = env_int("NS_GEMV_WHOLE", 1) != 0 && 4 * p.nslabs >= 3 * cus && p.nslabs <= 2 * cus;
+    if (whole) {
+        p.W = max_waves < nb ? max_waves : nb;
+        p.G = p.nslabs;
+        return p;
+    }
+    p.W = kWgWaves;
     p.G = (cap + kWgWaves - 1) / kWgWaves;
     if (p.G > U) p.G = U;
     return p;
@@ -464,9 +482,10 @@ int resident_waves_for(int type, int layout, bool pair) {
 template <int TYPE, bool PAIR>
 hipError_t launch_typed(int layout, const uint8_t *w, const uint8_t *up, const float *x, float *out,
                         uint32_t cols, uint32_t rows, const Workspace &ws, hipStream_t stream) {
-    const GemvPlan p = plan_gemv(cols, rows, resident_waves<TYPE, PAIR>(layout));
+    const GemvPlan p = plan_gemv(cols, rows, resident_waves<TYPE, PAIR>(layout), max_wg_waves(TYPE, PAIR),
+                                 uint32_t(device_shape().cus));
     const uint32_t nb = cols / kQK;
-    const dim3 grid(p.G), block(kWgWaves * 64);
+    const dim3 grid(p.G), block(p.W * 64);
     if (layout == CDNA4)
         gemv_kernel<TYPE, CDNA4, PAIR><<<grid, block, 0, stream>>>(w, up, x, out, rows, nb, p.nslabs, ws.partial, ws.counters);
     else if (layout == NSMFFN)
@@ -480,7 +499,8 @@ hipError_t launch_typed(int layout, const uint8_t *w, const uint8_t *up, const f
 
 void gemv_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, bool pair, size_t *partial_floats,
                          size_t *counters) {
-    const GemvPlan p = plan_gemv(cols, rows, resident_waves_for(type, layout, pair));
+    const GemvPlan p = plan_gemv(cols, rows, resident_waves_for(type, layout, pair),
+                                 max_wg_waves(pair ? Q4_K : type, pair), uint32_t(device_shape().cus));
     *partial_floats = size_t(p.G) * 2 * 64 * (pair ? 2 : 1);
     *counters = p.nslabs;
 }

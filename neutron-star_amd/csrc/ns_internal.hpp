@@ -33,8 +33,17 @@ void gemv_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, boo
                          size_t *counters);
 
 // Workspace the prefill GEMM needs: Q4_K group sums of x, split-K parts, tile counters.
-void gemm_workspace_need(int type, uint32_t cols, uint32_t rows, uint32_t batch, bool pair, size_t *floats,
-                         size_t *counters);
+void gemm_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, uint32_t batch, bool pair,
+                         size_t *floats, size_t *counters);
+
+// The Q4_K CDNA4 prefill GEMM with register-resident weight fragments
+// (ns_gemm_reg.hip): split-K parts it needs, and the launch.  xsums: the two
+// fp16 planes of x group sums; partial: the split-K parts.
+void gemm_reg_workspace_need(uint32_t cols, uint32_t rows, uint32_t batch, bool pair, size_t *part_floats,
+                             size_t *counters);
+hipError_t launch_gemm_reg(int acc, const uint8_t *w, const uint8_t *up, const uint16_t *x, const uint16_t *xsums,
+                           void *out, uint32_t cols, uint32_t rows, uint32_t batch, float *partial,
+                           uint32_t *counters, hipStream_t stream);
 
 // Prefill GEMM over fp16 x [batch][cols]: plain (fp32 out [batch][rows]) or the
 // gate/up pair with GeGLU (fp16 h [batch][rows]).

@@ -17,7 +17,7 @@
 //
 // One workgroup per token; both sums are taken in fp32 in a fixed order
 // (deterministic), the second about the mean so the common component does not
-// cancel precision away.
+// cancel precision away.  The output row must not alias the input row.
 #include "ns_internal.hpp"
 #include "ns_quant.hpp"
 
@@ -37,12 +37,56 @@ __device__ __forceinline__ float block_sum(float s, float *part) {
     return tot;
 }
 
+// Rows of up to kThreads * 4 * kMaxVec values are read once into registers
+// (float4 per thread, coalesced); longer or unaligned rows take the looped path.
+constexpr int kMaxVec = 8;  // float4 loads per thread: rows of up to 8192 values
+
 template <bool HALF>
 __global__ __launch_bounds__(kThreads) void standardize_kernel(const float *__restrict__ y, uint32_t cols,
-                                                             void *__restrict__ out) {
+                                                             void *__restrict__ out, bool vec_ok) {
     __shared__ float part[kThreads / 64];
     const uint32_t t = blockIdx.x, tid = threadIdx.x;
     const float *row = y + size_t(t) * cols;
+    const uint32_t n4 = cols / 4;
+    if (vec_ok && cols % 4 == 0 && n4 <= uint32_t(kThreads * kMaxVec)) {
+        float4 v[kMaxVec];
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < kMaxVec; ++i) {
+            const uint32_t j = tid + uint32_t(i) * kThreads;
+            v[i] = j < n4 ? reinterpret_cast<const float4 *>(row)[j] : float4{0.f, 0.f, 0.f, 0.f};
+            s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+        }
+        const float mean = block_sum(s, part) / float(cols);
+        float q = 0.f;
+#pragma unroll
+        for (int i = 0; i < kMaxVec; ++i) {
+            if (tid + uint32_t(i) * kThreads >= n4) continue;
+            v[i].x -= mean;
+            v[i].y -= mean;
+            v[i].z -= mean;
+            v[i].w -= mean;
+            q = __builtin_fmaf(v[i].x, v[i].x, q);
+            q = __builtin_fmaf(v[i].y, v[i].y, q);
+            q = __builtin_fmaf(v[i].z, v[i].z, q);
+            q = __builtin_fmaf(v[i].w, v[i].w, q);
+        }
+        const float var = block_sum(q, part) / float(cols);
+        const float inv = var > 0.f ? 1.0f / __builtin_sqrtf(var) : 0.f;
+#pragma unroll
+        for (int i = 0; i < kMaxVec; ++i) {
+            const uint32_t j = tid + uint32_t(i) * kThreads;
+            if (j >= n4) continue;
+            const float a = v[i].x * inv, b = v[i].y * inv, c = v[i].z * inv, d = v[i].w * inv;
+            if constexpr (HALF) {
+                typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+                reinterpret_cast<half4_t *>(out)[size_t(t) * n4 + j] = half4_t{_Float16(a), _Float16(b), _Float16(c), _Float16(d)};
+            } else {
+                reinterpret_cast<float4 *>(out)[size_t(t) * n4 + j] = float4{a, b, c, d};
+            }
+        }
+        return;
+    }
     float s = 0.f;
     for (uint32_t k = tid; k < cols; k += kThreads) s += row[k];
     const float mean = block_sum(s, part) / float(cols);
@@ -64,8 +108,10 @@ __global__ __launch_bounds__(kThreads) void standardize_kernel(const float *__re
 
 hipError_t launch_standardize(const float *y, uint32_t batch, uint32_t cols, void *out, bool half,
                               hipStream_t stream) {
-    if (half) standardize_kernel<true><<<dim3(batch), dim3(kThreads), 0, stream>>>(y, cols, out);
-    else standardize_kernel<false><<<dim3(batch), dim3(kThreads), 0, stream>>>(y, cols, out);
+    // float4 / half4 accesses need 16-byte aligned input and output rows
+    const bool vec_ok = (reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(out)) % 16 == 0;
+    if (half) standardize_kernel<true><<<dim3(batch), dim3(kThreads), 0, stream>>>(y, cols, out, vec_ok);
+    else standardize_kernel<false><<<dim3(batch), dim3(kThreads), 0, stream>>>(y, cols, out, vec_ok);
     return hipGetLastError();
 }
 
