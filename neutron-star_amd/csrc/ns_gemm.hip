@@ -469,57 +469,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
         else return r0 + bcol(jj) + (lane & 31);
     };
 
-    if (kparts > 1) {
-        // partial layout [kp][jj-plane (PAIR: gate, up)][batch][rows]
-        constexpr uint32_t kPlanes = PAIR ? 2 : 1;
-        auto pidx = [&](uint32_t part, int jj, uint32_t t, uint32_t r) -> size_t {
-            return ((size_t(part) * kPlanes + (PAIR ? uint32_t(jj) : 0u)) * batch + t) * rows + r;
-        };
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const uint32_t t = tok_of(i, v);
-#pragma unroll
-                for (int jj = 0; jj < NJ; ++jj) {
-                    const uint32_t r = col_row(jj);
-                    if (t < batch && r < rows)
-                        __hip_atomic_store(&partial[pidx(kp, jj, t, r)], acc[i][jj][v], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-                }
-            }
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_s_waitcnt(0);
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __syncthreads();  // every wave's parts are stored
-        if (tid == 0) {
-            const uint32_t prev =
-                __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            last_flag = prev == kparts - 1;
-        }
-        __syncthreads();
-        if (!last_flag) return;
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const uint32_t t = tok_of(i, v);
-#pragma unroll
-                for (int jj = 0; jj < NJ; ++jj) {
-                    const uint32_t r = col_row(jj);
-                    float sum = 0.f;
-                    if (t < batch && r < rows)
-                        for (uint32_t part = 0; part < kparts; ++part)
-                            sum += __hip_atomic_load(&partial[pidx(part, jj, t, r)], __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-                    acc[i][jj][v] = ACC == ACC_FP16 ? round_f16p(sum) : sum;
-                }
-            }
-        if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-
-#pragma unroll
-    for (int i = 0; i < MI; ++i) {
+    // Outputs of token sub-tile i: fp16 GeGLU (PAIR) or fp32 per column.
+    auto write_out = [&](int i) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             const uint32_t t = tok_of(i, v);
@@ -537,6 +488,75 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
                 }
             }
         }
+    };
+
+    if (kparts == 1) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i) write_out(i);
+        return;
+    }
+
+    // ---- split K.  Parts [kp][plane (PAIR: gate, up)][batch][rows]; one part is
+    // under 4 GiB (checked by the host plan), so a position within it is a 32-bit
+    // byte offset from the part's (wave-uniform) base.
+    constexpr uint32_t kPlanes = PAIR ? 2 : 1;
+    const size_t pstride = size_t(kPlanes) * batch * rows;  // floats per part
+    auto pat = [&](uint32_t part, int jj, uint32_t t, uint32_t r) -> float * {
+        const uint32_t off = (((PAIR ? uint32_t(jj) : 0u) * batch + t) * rows + r) * 4u;
+        return reinterpret_cast<float *>(reinterpret_cast<char *>(partial + part * pstride) + off);
+    };
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const uint32_t t = tok_of(i, v);
+#pragma unroll
+            for (int jj = 0; jj < NJ; ++jj) {
+                const uint32_t r = col_row(jj);
+                if (t < batch && r < rows)
+                    __hip_atomic_store(pat(kp, jj, t, r), acc[i][jj][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();  // every wave's parts are stored
+    if (tid == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_flag = prev == kparts - 1;
+    }
+    __syncthreads();
+    if (!last_flag) return;
+    if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Last arrival: per token sub-tile, the parts are added in part order
+    // (deterministic), every load of one part in flight before any is added, and
+    // the sub-tile is written out at once.  Token and row indices are clamped so
+    // every load is in bounds (clamped positions were never stored and are never
+    // written out).
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+        float sum[16][NJ];
+        for (uint32_t part = 0; part < kparts; ++part) {
+            float pv[16][NJ];
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const uint32_t t = __builtin_elementwise_min(tok_of(i, v), batch - 1);
+#pragma unroll
+                for (int jj = 0; jj < NJ; ++jj)
+                    pv[v][jj] = __hip_atomic_load(pat(part, jj, t, __builtin_elementwise_min(col_row(jj), rows - 1)),
+                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+#pragma unroll
+                for (int jj = 0; jj < NJ; ++jj) sum[v][jj] = (part == 0 ? 0.f : sum[v][jj]) + pv[v][jj];
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+#pragma unroll
+            for (int jj = 0; jj < NJ; ++jj)
+                acc[i][jj][v] = ACC == ACC_FP16 ? round_f16p(sum[v][jj]) : sum[v][jj];
+        write_out(i);
     }
 }
 
@@ -579,6 +599,8 @@ GemmPlan plan_gemm(uint32_t cols, uint32_t rows, uint32_t batch, bool pair) {
         const int v = atoi(e);
         if (v >= 1 && uint32_t(v) <= nb) p.kparts = uint32_t(v);
     }
+    // one split-K part must stay under 4 GiB (32-bit offsets inside the kernel)
+    if (uint64_t(pair ? 2 : 1) * batch * rows * 4 >= (uint64_t(1) << 32)) p.kparts = 1;
     return p;
 }
 

@@ -328,26 +328,32 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
         }
     };
 
+    // outputs of token sub-tile i
+    auto write_out = [&](int i) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            float val[NJ];
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) val[j] = acc[i][j][v];
+            emit(tok_of(i, v), val);
+        }
+    };
+
     if (kparts == 1) {
 #pragma unroll
-        for (int i = 0; i < MI; ++i)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                float val[NJ];
-#pragma unroll
-                for (int j = 0; j < NJ; ++j) val[j] = acc[i][j][v];
-                emit(tok_of(i, v), val);
-            }
+        for (int i = 0; i < MI; ++i) write_out(i);
         return;
     }
 
-    // ---- split K: parts [kp][plane][batch][rows]; the last workgroup of a tile to
-    // arrive adds them in part order (deterministic) and writes the output.
-    // PAIR: gate and up of the same row are two planes; plain: the two column tiles
-    // are different rows of one plane (the workspace holds kparts * planes * batch * rows)
+    // ---- split K: parts [kp][plane][batch][rows].  PAIR: gate and up of the same
+    // row are two planes; plain: the two column tiles are different rows of one
+    // plane.  One part is under 4 GiB (checked by the host plan), so a position
+    // within it is a 32-bit byte offset from the part's (wave-uniform) base.
     constexpr uint32_t kPlanes = PAIR ? 2 : 1;
-    auto pidx = [&](uint32_t part, int j, uint32_t t, uint32_t r) -> size_t {
-        return ((size_t(part) * kPlanes + (PAIR ? uint32_t(j) : 0u)) * batch + t) * rows + r;
+    const size_t pstride = size_t(kPlanes) * batch * rows;  // floats per part
+    auto pat = [&](uint32_t part, int j, uint32_t t, uint32_t r) -> float * {
+        const uint32_t off = (((PAIR ? uint32_t(j) : 0u) * batch + t) * rows + r) * 4u;
+        return reinterpret_cast<float *>(reinterpret_cast<char *>(partial + part * pstride) + off);
     };
 #pragma unroll
     for (int i = 0; i < MI; ++i)
@@ -358,7 +364,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
             for (int j = 0; j < NJ; ++j) {
                 const uint32_t r = brow(j);
                 if (t < batch && r < rows)
-                    __hip_atomic_store(&partial[pidx(kp, j, t, r)], acc[i][j][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(pat(kp, j, t, r), acc[i][j][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
     // Device-coherent atomics only: the parts bypass the XCD-private L2; the wait
@@ -373,30 +379,35 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
     }
     __syncthreads();
     if (!last_flag) return;
-    for (int i = 0; i < MI; ++i)
-        for (int v = 0; v < 16; ++v) {
-            const uint32_t t = tok_of(i, v);
-            float val[NJ];
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                const uint32_t r = brow(j);
-                float sum = 0.f;
-                if (t < batch && r < rows)
-                    for (uint32_t k0 = 0; k0 < kparts; k0 += 4) {  // 4 loads in flight, added in order
-                        float pv[4];
-#pragma unroll
-                        for (uint32_t u = 0; u < 4; ++u)
-                            pv[u] = k0 + u < kparts ? __hip_atomic_load(&partial[pidx(k0 + u, j, t, r)], __ATOMIC_RELAXED,
-                                                                        __HIP_MEMORY_SCOPE_AGENT)
-                                                    : 0.f;
-#pragma unroll
-                        for (uint32_t u = 0; u < 4; ++u) sum += pv[u];
-                    }
-                val[j] = ACC == ACC_FP16 ? round_f16p(sum) : sum;
-            }
-            emit(t, val);
-        }
     if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Last arrival: per token sub-tile, the parts are added in part order
+    // (deterministic), every load of one part in flight before any is added, and
+    // the sub-tile is written out at once.  Indices are clamped so every load is in
+    // bounds (clamped positions were never stored and are never written out).
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+        float sum[16][NJ];
+        for (uint32_t part = 0; part < kparts; ++part) {
+            float pv[16][NJ];
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const uint32_t t = __builtin_elementwise_min(tok_of(i, v), batch - 1);
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+                    pv[v][j] = __hip_atomic_load(pat(part, j, t, __builtin_elementwise_min(brow(j), rows - 1)),
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) sum[v][j] = (part == 0 ? 0.f : sum[v][j]) + pv[v][j];
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) acc[i][j][v] = ACC == ACC_FP16 ? round_f16p(sum[v][j]) : sum[v][j];
+        write_out(i);
+    }
 }
 
 struct RegPlan {
@@ -416,6 +427,8 @@ RegPlan plan_reg(uint32_t cols, uint32_t rows, uint32_t batch, bool pair) {
         const int v = atoi(e);
         if (v >= 1 && uint32_t(v) <= nb) p.kparts = uint32_t(v);
     }
+    // one split-K part must stay under 4 GiB (32-bit offsets inside the kernel)
+    if (uint64_t(pair ? 2 : 1) * batch * rows * 4 >= (uint64_t(1) << 32)) p.kparts = 1;
     return p;
 }
 
