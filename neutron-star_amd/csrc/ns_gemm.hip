@@ -469,8 +469,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
         else return r0 + bcol(jj) + (lane & 31);
     };
 
-    // Outputs of token sub-tile i: fp16 GeGLU (PAIR) or fp32 per column.
-    auto write_out = [&](int i) {
+    // Outputs of token sub-tile i: fp16 GeGLU (PAIR) or fp32 per column, from
+    // val(v, jj) = the value of accumulator element v of column fragment jj.
+    auto write_out = [&](int i, auto val) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             const uint32_t t = tok_of(i, v);
@@ -478,13 +479,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
             if constexpr (PAIR) {
                 const uint32_t r = col_row(0);
                 if (r < rows)
-                    reinterpret_cast<_Float16 *>(out)[size_t(t) * rows + r] =
-                        _Float16(gelu_tanh(acc[i][0][v]) * acc[i][1][v]);
+                    reinterpret_cast<_Float16 *>(out)[size_t(t) * rows + r] = _Float16(gelu_tanh(val(v, 0)) * val(v, 1));
             } else {
 #pragma unroll
                 for (int jj = 0; jj < NJ; ++jj) {
                     const uint32_t r = col_row(jj);
-                    if (r < rows) reinterpret_cast<float *>(out)[size_t(t) * rows + r] = acc[i][jj][v];
+                    if (r < rows) reinterpret_cast<float *>(out)[size_t(t) * rows + r] = val(v, jj);
                 }
             }
         }
@@ -492,29 +492,39 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
 
     if (kparts == 1) {
 #pragma unroll
-        for (int i = 0; i < MI; ++i) write_out(i);
+        for (int i = 0; i < MI; ++i) write_out(i, [&](int v, int jj) { return acc[i][jj][v]; });
         return;
     }
 
-    // ---- split K.  Parts [kp][plane (PAIR: gate, up)][batch][rows]; one part is
-    // under 4 GiB (checked by the host plan), so a position within it is a 32-bit
-    // byte offset from the part's (wave-uniform) base.
+    // ---- split K.  Parts [kp][plane][ntok*TT][ncol*rows per tile] (PAIR: gate, up):
+    // padded to whole tiles, so every position of a tile has a slot and no part
+    // store or load needs a guard.  One part is under 4 GiB (checked by the host
+    // plan), so a slot is a 32-bit byte offset from the part's (uniform) base.
     constexpr uint32_t kPlanes = PAIR ? 2 : 1;
-    const size_t pstride = size_t(kPlanes) * batch * rows;  // floats per part
-    auto pat = [&](uint32_t part, int jj, uint32_t t, uint32_t r) -> float * {
-        const uint32_t off = (((PAIR ? uint32_t(jj) : 0u) * batch + t) * rows + r) * 4u;
-        return reinterpret_cast<float *>(reinterpret_cast<char *>(partial + part * pstride) + off);
+    const uint32_t tpad = ntok_tiles * TT, rpad = ncol_tiles * kRowsPerTile;
+    const size_t pstride = size_t(kPlanes) * tpad * rpad;  // floats per part
+    // Slot of (part, plane, token tok_of(i, v), column): the part's wave-uniform
+    // base plus a 32-bit byte offset (lane_off holds the lane's plane, token and
+    // column terms).
+    const uint32_t rstride = rpad * 4u;
+    uint32_t lane_off[NJ];
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj)
+        lane_off[jj] = ((PAIR ? uint32_t(jj) : 0u) * tpad + t0 + wt * WT + 4 * (lane >> 5)) * rstride + col_row(jj) * 4u;
+    // byte offset of (token sub-tile i, element v, fragment jj) within one part,
+    // given the lane terms lo
+    auto poff = [&](const uint32_t (&lo)[NJ], int i, int v, int jj) -> uint32_t {
+        return (uint32_t(i) * 32 + 8 * uint32_t(v >> 2) + uint32_t(v & 3)) * rstride + lo[jj];
     };
+    auto pbase = [&](uint32_t part) -> char * { return reinterpret_cast<char *>(partial + part * pstride); };  // uniform
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-            const uint32_t t = tok_of(i, v);
 #pragma unroll
             for (int jj = 0; jj < NJ; ++jj) {
-                const uint32_t r = col_row(jj);
-                if (t < batch && r < rows)
-                    __hip_atomic_store(pat(kp, jj, t, r), acc[i][jj][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(reinterpret_cast<float *>(pbase(kp) + poff(lane_off, i, v, jj)), acc[i][jj][v],
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -528,35 +538,41 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     __syncthreads();
     if (!last_flag) return;
     if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // Last arrival: per token sub-tile, the parts are added in part order
-    // (deterministic), every load of one part in flight before any is added, and
-    // the sub-tile is written out at once.  Token and row indices are clamped so
-    // every load is in bounds (clamped positions were never stored and are never
-    // written out).
+    // Last arrival: the parts are added in part order (deterministic).  One round
+    // trip loads one part of two token sub-tiles (64 values per lane, all in flight
+    // before any is added); the two sub-tiles are then written out.
 #pragma unroll
-    for (int i = 0; i < MI; ++i) {
-        float sum[16][NJ];
+    for (int i0 = 0; i0 < MI; i0 += 2) {
+        float sum[2][16][NJ];
         for (uint32_t part = 0; part < kparts; ++part) {
-            float pv[16][NJ];
+            // the lane terms pass through an empty asm, so the compiler recomputes
+            // the 64 offsets in each iteration instead of keeping them all live
+            uint32_t lo[NJ];
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const uint32_t t = __builtin_elementwise_min(tok_of(i, v), batch - 1);
-#pragma unroll
-                for (int jj = 0; jj < NJ; ++jj)
-                    pv[v][jj] = __hip_atomic_load(pat(part, jj, t, __builtin_elementwise_min(col_row(jj), rows - 1)),
-                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int jj = 0; jj < NJ; ++jj) {
+                lo[jj] = lane_off[jj];
+                asm volatile("" : "+v"(lo[jj]));
             }
+            float pv[2][16][NJ];
 #pragma unroll
-            for (int v = 0; v < 16; ++v)
+            for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-                for (int jj = 0; jj < NJ; ++jj) sum[v][jj] = (part == 0 ? 0.f : sum[v][jj]) + pv[v][jj];
+                for (int v = 0; v < 16; ++v)
+#pragma unroll
+                    for (int jj = 0; jj < NJ; ++jj)
+                        pv[ii][v][jj] = __hip_atomic_load(reinterpret_cast<float *>(pbase(part) + poff(lo, i0 + ii, v, jj)),
+                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+#pragma unroll
+                    for (int jj = 0; jj < NJ; ++jj)
+                        sum[ii][v][jj] = (part == 0 ? 0.f : sum[ii][v][jj]) + pv[ii][v][jj];
         }
 #pragma unroll
-        for (int v = 0; v < 16; ++v)
-#pragma unroll
-            for (int jj = 0; jj < NJ; ++jj)
-                acc[i][jj][v] = ACC == ACC_FP16 ? round_f16p(sum[v][jj]) : sum[v][jj];
-        write_out(i);
+        for (int ii = 0; ii < 2; ++ii)
+            write_out(i0 + ii, [&](int v, int jj) { return ACC == ACC_FP16 ? round_f16p(sum[ii][v][jj]) : sum[ii][v][jj]; });
     }
 }
 
@@ -599,8 +615,8 @@ GemmPlan plan_gemm(uint32_t cols, uint32_t rows, uint32_t batch, bool pair) {
         const int v = atoi(e);
         if (v >= 1 && uint32_t(v) <= nb) p.kparts = uint32_t(v);
     }
-    // one split-K part must stay under 4 GiB (32-bit offsets inside the kernel)
-    if (uint64_t(pair ? 2 : 1) * batch * rows * 4 >= (uint64_t(1) << 32)) p.kparts = 1;
+    // one split-K part (padded to whole tiles) must stay under 4 GiB: 32-bit offsets in the kernel
+    if (uint64_t(pair ? 2 : 1) * p.ntok * TT * p.ncol * rows_per_tile * 4 >= (uint64_t(1) << 32)) p.kparts = 1;
     return p;
 }
 
@@ -633,14 +649,23 @@ hipError_t launch_layout(int layout, int acc, const uint8_t *w, const uint8_t *u
 }  // namespace
 
 // Workspace layout: [Q4_K group sums of x: 2 fp16 planes of batch x cols/32,
-// counted in floats and rounded up to 64] [split-K parts: kparts x planes x batch x rows].
+// counted in floats and rounded up to 64] [split-K parts: kparts x planes x tokens x rows,
+// both padded to whole tiles].
 static size_t xs_floats(int type, uint32_t cols, uint32_t batch) {
     return type == Q4_K ? ((size_t(batch) * (cols / 32) + 63) / 64) * 64 : 0;
 }
 
+// Q4_K on the CDNA4 layout runs the register-fragment kernel (ns_gemm_reg.hip)
+// unless NS_GEMM_Q4_REG=0 selects the LDS-tile kernel here.
+static bool use_gemm_reg(int type, int layout) {
+    if (layout != CDNA4 || type != Q4_K) return false;
+    const char *e = getenv("NS_GEMM_Q4_REG");
+    return !(e && e[0] == '0');
+}
+
 void gemm_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, uint32_t batch, bool pair,
                          size_t *floats, size_t *counters) {
-    if (layout == CDNA4 && type == Q4_K) {
+    if (use_gemm_reg(type, layout)) {
         size_t part = 0;
         gemm_reg_workspace_need(cols, rows, batch, pair, &part, counters);
         *floats = xs_floats(type, cols, batch) + part;
@@ -648,7 +673,7 @@ void gemm_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, uin
     }
     const GemmPlan p = plan_gemm(cols, rows, batch, pair);
     *floats = xs_floats(type, cols, batch) +
-              (p.kparts > 1 ? size_t(p.kparts) * (pair ? 2 : 1) * batch * rows : 0);
+              (p.kparts > 1 ? size_t(p.kparts) * (pair ? 2 : 1) * (p.ntok * TT) * (p.ncol * (pair ? TC / 2 : TC)) : 0);
     *counters = size_t(p.ntok) * p.ncol;
 }
 
@@ -664,8 +689,7 @@ hipError_t launch_gemm(int type, int layout, int acc, const uint8_t *w, const ui
         if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     }
     const size_t off = xs_floats(type, cols, batch);
-    // Q4_K on the CDNA4 layout: register-resident weight fragments (ns_gemm_reg.hip)
-    if (layout == CDNA4 && type == Q4_K)
+    if (use_gemm_reg(type, layout))
         return launch_gemm_reg(acc, w, up, x, xh, out, cols, rows, batch, ws.partial + off, ws.counters, stream);
     if (up) return launch_layout<Q4_K, true>(layout, acc, w, up, x, xh, out, cols, rows, batch, ws, off, stream);
     if (type == Q4_K)

@@ -328,43 +328,52 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
         }
     };
 
-    // outputs of token sub-tile i
-    auto write_out = [&](int i) {
+    // outputs of token sub-tile i, from get(v, j) = accumulator element v of fragment j
+    auto write_out = [&](int i, auto get) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             float val[NJ];
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) val[j] = acc[i][j][v];
+            for (int j = 0; j < NJ; ++j) val[j] = get(v, j);
             emit(tok_of(i, v), val);
         }
     };
 
     if (kparts == 1) {
 #pragma unroll
-        for (int i = 0; i < MI; ++i) write_out(i);
+        for (int i = 0; i < MI; ++i) write_out(i, [&](int v, int j) { return acc[i][j][v]; });
         return;
     }
 
-    // ---- split K: parts [kp][plane][batch][rows].  PAIR: gate and up of the same
-    // row are two planes; plain: the two column tiles are different rows of one
-    // plane.  One part is under 4 GiB (checked by the host plan), so a position
-    // within it is a 32-bit byte offset from the part's (wave-uniform) base.
+    // ---- split K.  Parts [kp][plane][ntok*TT][ncol*rows per tile] (PAIR: gate, up; plain: one plane):
+    // padded to whole tiles, so every position of a tile has a slot and no part
+    // store or load needs a guard.  One part is under 4 GiB (checked by the host
+    // plan), so a slot is a 32-bit byte offset from the part's (uniform) base.
     constexpr uint32_t kPlanes = PAIR ? 2 : 1;
-    const size_t pstride = size_t(kPlanes) * batch * rows;  // floats per part
-    auto pat = [&](uint32_t part, int j, uint32_t t, uint32_t r) -> float * {
-        const uint32_t off = (((PAIR ? uint32_t(j) : 0u) * batch + t) * rows + r) * 4u;
-        return reinterpret_cast<float *>(reinterpret_cast<char *>(partial + part * pstride) + off);
+    const uint32_t tpad = ntok_tiles * TT, rpad = ncol_tiles * kRowsPerTile;
+    const size_t pstride = size_t(kPlanes) * tpad * rpad;  // floats per part
+    // Slot of (part, plane, token tok_of(i, v), column): the part's wave-uniform
+    // base plus a 32-bit byte offset (lane_off holds the lane's plane, token and
+    // column terms).
+    const uint32_t rstride = rpad * 4u;
+    uint32_t lane_off[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+        lane_off[j] = ((PAIR ? uint32_t(j) : 0u) * tpad + t0 + 4 * hl) * rstride + brow(j) * 4u;
+    // byte offset of (token sub-tile i, element v, fragment j) within one part,
+    // given the lane terms lo
+    auto poff = [&](const uint32_t (&lo)[NJ], int i, int v, int j) -> uint32_t {
+        return (uint32_t(i) * 32 + 8 * uint32_t(v >> 2) + uint32_t(v & 3)) * rstride + lo[j];
     };
+    auto pbase = [&](uint32_t part) -> char * { return reinterpret_cast<char *>(partial + part * pstride); };  // uniform
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-            const uint32_t t = tok_of(i, v);
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
-                const uint32_t r = brow(j);
-                if (t < batch && r < rows)
-                    __hip_atomic_store(pat(kp, j, t, r), acc[i][j][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(reinterpret_cast<float *>(pbase(kp) + poff(lane_off, i, v, j)), acc[i][j][v],
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
     // Device-coherent atomics only: the parts bypass the XCD-private L2; the wait
@@ -380,33 +389,41 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
     __syncthreads();
     if (!last_flag) return;
     if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // Last arrival: per token sub-tile, the parts are added in part order
-    // (deterministic), every load of one part in flight before any is added, and
-    // the sub-tile is written out at once.  Indices are clamped so every load is in
-    // bounds (clamped positions were never stored and are never written out).
+    // Last arrival: the parts are added in part order (deterministic).  One round
+    // trip loads one part of two token sub-tiles (64 values per lane, all in flight
+    // before any is added); the two sub-tiles are then written out.
 #pragma unroll
-    for (int i = 0; i < MI; ++i) {
-        float sum[16][NJ];
+    for (int i0 = 0; i0 < MI; i0 += 2) {
+        float sum[2][16][NJ];
         for (uint32_t part = 0; part < kparts; ++part) {
-            float pv[16][NJ];
+            // the lane terms pass through an empty asm, so the compiler recomputes
+            // the 64 offsets in each iteration instead of keeping them all live
+            uint32_t lo[NJ];
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const uint32_t t = __builtin_elementwise_min(tok_of(i, v), batch - 1);
-#pragma unroll
-                for (int j = 0; j < NJ; ++j)
-                    pv[v][j] = __hip_atomic_load(pat(part, j, t, __builtin_elementwise_min(brow(j), rows - 1)),
-                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int j = 0; j < NJ; ++j) {
+                lo[j] = lane_off[j];
+                asm volatile("" : "+v"(lo[j]));
             }
+            float pv[2][16][NJ];
 #pragma unroll
-            for (int v = 0; v < 16; ++v)
+            for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-                for (int j = 0; j < NJ; ++j) sum[v][j] = (part == 0 ? 0.f : sum[v][j]) + pv[v][j];
+                for (int v = 0; v < 16; ++v)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j)
+                        pv[ii][v][j] = __hip_atomic_load(reinterpret_cast<float *>(pbase(part) + poff(lo, i0 + ii, v, j)),
+                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j)
+                        sum[ii][v][j] = (part == 0 ? 0.f : sum[ii][v][j]) + pv[ii][v][j];
         }
 #pragma unroll
-        for (int v = 0; v < 16; ++v)
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) acc[i][j][v] = ACC == ACC_FP16 ? round_f16p(sum[v][j]) : sum[v][j];
-        write_out(i);
+        for (int ii = 0; ii < 2; ++ii)
+            write_out(i0 + ii, [&](int v, int j) { return ACC == ACC_FP16 ? round_f16p(sum[ii][v][j]) : sum[ii][v][j]; });
     }
 }
 
@@ -427,8 +444,8 @@ RegPlan plan_reg(uint32_t cols, uint32_t rows, uint32_t batch, bool pair) {
         const int v = atoi(e);
         if (v >= 1 && uint32_t(v) <= nb) p.kparts = uint32_t(v);
     }
-    // one split-K part must stay under 4 GiB (32-bit offsets inside the kernel)
-    if (uint64_t(pair ? 2 : 1) * batch * rows * 4 >= (uint64_t(1) << 32)) p.kparts = 1;
+    // one split-K part (padded to whole tiles) must stay under 4 GiB: 32-bit offsets in the kernel
+    if (uint64_t(pair ? 2 : 1) * p.ntok * TT * p.ncol * rows_per_tile * 4 >= (uint64_t(1) << 32)) p.kparts = 1;
     return p;
 }
 
@@ -437,7 +454,7 @@ RegPlan plan_reg(uint32_t cols, uint32_t rows, uint32_t batch, bool pair) {
 void gemm_reg_workspace_need(uint32_t cols, uint32_t rows, uint32_t batch, bool pair, size_t *part_floats,
                              size_t *counters) {
     const RegPlan p = plan_reg(cols, rows, batch, pair);
-    *part_floats = p.kparts > 1 ? size_t(p.kparts) * (pair ? 2 : 1) * batch * rows : 0;
+    *part_floats = p.kparts > 1 ? size_t(p.kparts) * (pair ? 2 : 1) * (p.ntok * TT) * (p.ncol * (pair ? TC / 2 : TC)) : 0;
     *counters = size_t(p.ntok) * p.ncol;
 }
 

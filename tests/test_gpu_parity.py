@@ -197,6 +197,40 @@ def test_prefill_down_small(ctx, cols, rows, batch, qtype, acc, layout):
         assert rel_err(got, ref16) <= 4e-3
 
 
+# Forced split-K: every part count path of both Q4_K kernels (register-fragment,
+# LDS-tile) and the Q6_K kernel, on ragged token and row tiles.  Parts of 1 or 2
+# super-blocks each; the last workgroup of a tile adds them in part order.
+SPLIT_CASES = [("q4k-reg", N.Q4_K, "1"), ("q4k-lds", N.Q4_K, "0"), ("q6k-lds", N.Q6_K, "1")]
+
+
+@pytest.mark.parametrize("kparts", ["3", "5"])
+@pytest.mark.parametrize("acc", [N.ACC_FP32, N.ACC_FP16], ids=["fp32acc", "fp16acc"])
+@pytest.mark.parametrize("name,qtype,reg", SPLIT_CASES, ids=[c[0] for c in SPLIT_CASES])
+def test_prefill_split_k(ctx, monkeypatch, name, qtype, reg, acc, kparts):
+    monkeypatch.setenv("NS_GEMM_KPARTS", kparts)
+    monkeypatch.setenv("NS_GEMM_Q4_REG", reg)
+    cols, rows, batch = 2048, 320, 200
+    fast = acc == N.ACC_FP16
+    tol = TOL16 if fast else TOL32
+    x = N.synth_normal_f16(71, batch * cols).reshape(batch, cols)
+    hw, w = weights(qtype, 72, rows, cols, N.CDNA4)
+    y = torch.empty((batch, rows), dtype=torch.float32, device="cuda")
+    ctx.ffn_down(w, qtype, N.CDNA4, cols, rows, batch, dev_u16(x), y, half_input=True, fast_swa=fast)
+    if qtype == N.Q4_K:
+        hu, wu = weights(N.Q4_K, 73, rows, cols, N.CDNA4)
+        h = torch.empty((batch, rows), dtype=torch.int16, device="cuda")
+        ctx.gate_up_geglu_rm32(w, wu, N.CDNA4, cols, rows, batch, dev_u16(x), h, fast_swa=fast)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    assert rel_err(got, O.gemm(qtype, O.ROW_MAJOR, hw, cols, rows, batch, x, 0)) <= tol
+    if fast:
+        assert not np.any(got.view(np.uint32) & 0x1FFF)
+        assert rel_err(got, O.gemm(qtype, O.ROW_MAJOR, hw, cols, rows, batch, x, 1)) <= 4e-3
+    if qtype == N.Q4_K:
+        hh = f16_value(h.cpu().numpy().view(np.uint16))
+        assert rel_err(hh, O.gate_up_geglu_prefill(O.ROW_MAJOR, hw, hu, cols, rows, batch, x, 0)) <= tol
+
+
 def _row_slice(host, qtype, cols, r0, nrows):
     bpr = (cols // 256) * N.BLOCK_BYTES[qtype]
     return np.ascontiguousarray(host[r0 * bpr:(r0 + nrows) * bpr])
