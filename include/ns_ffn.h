@@ -74,8 +74,10 @@ int ns_ctx_destroy(ns_ctx *ctx);
 
 /* NativeMetalEngine::matmul (mm:269-275): out = in . W^T for `batch` tokens.
  *   batch == 1, fp32 input      -> dequant-fused GEMV (decode; lm-head with ROW_MAJOR or CDNA4).
- *   batch  > 1, half_input != 0 -> dequant-into-LDS MFMA GEMM, FP32 accumulation.
- *   batch  > 1, fp32 input      -> one GEMV per token.
+ *   batch 2-4, fp32 or fp16     -> small-batch GEMV streaming the weights once for all tokens
+ *                                  (gemma_q4k/q6k_mm_fast[_f16][_metal], metal:125-177, mm:273).
+ *   batch  > 4, half_input != 0 -> dequant-into-LDS MFMA GEMM, FP32 accumulation.
+ *   batch  > 4, fp32 input      -> one GEMV per token.
  * `in` is fp32 [batch][cols] or, with half_input, fp16 bits [batch][cols]; out fp32 [batch][rows]. */
 int ns_matmul(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, uint32_t rows,
               uint32_t batch, const void *in, int half_input, float *out, void *stream);
@@ -85,6 +87,13 @@ int ns_gate_up_geglu_decode(ns_ctx *ctx, const void *wg, const void *wu, int lay
                             uint32_t cols, uint32_t rows, const float *x, float *h,
                             void *stream);
 
+/* gate_up_geglu (mm:281-286): H = gelu_tanh(X.Wg^T) * (X.Wu^T), x and h fp16 bits
+ * ([batch][cols], [batch][rows]).  batch <= 4 (MTP verification): the small-batch pair kernel,
+ * weights streamed once for all tokens (gemma_q4k_gate_up_geglu_mm_f16[_metal], metal:102-112,
+ * mm:282); larger batches: the prefill GEMM in the FP32 mode. */
+int ns_gate_up_geglu(ns_ctx *ctx, const void *wg, const void *wu, int layout, uint32_t cols, uint32_t rows,
+                     uint32_t batch, const uint16_t *x, uint16_t *h, void *stream);
+
 /* gate_up_geglu_rm32 (mm:288): prefill H = gelu_tanh(X.Wg^T) * (X.Wu^T).
  * x fp16 bits [batch][cols], h fp16 bits [batch][rows]; fast_swa != 0 selects
  * NS_ACC_FP16 (metal:379), 0 selects NS_ACC_FP32 (metal:373). */
@@ -92,7 +101,7 @@ int ns_gate_up_geglu_rm32(ns_ctx *ctx, const void *wg, const void *wu, int layou
                           uint32_t cols, uint32_t rows, uint32_t batch, const uint16_t *x,
                           uint16_t *h, int fast_swa, void *stream);
 
-/* ffn_down (mm:289): with half_input and batch > 1 the prefill GEMM in the mode
+/* ffn_down (mm:289): with half_input and batch > 4 the prefill GEMM in the mode
  * fast_swa selects (metal:480/486 Q6_K, :385/:391 Q4_K); otherwise ns_matmul. */
 int ns_ffn_down(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, uint32_t rows,
                 uint32_t batch, const void *in, int half_input, int fast_swa, float *out,

@@ -79,6 +79,17 @@ int gemv(ns_ctx *ctx, const char *fn, int type, int layout, const void *w, const
     return e == hipSuccess ? NS_OK : hip_fail(e, fn);
 }
 
+// Batch 2-4: the weights stream once for every token (mm:273, mm:282).
+int gemv_mt(ns_ctx *ctx, const char *fn, int type, int layout, const void *w, const void *up, const void *x,
+            bool xh, uint32_t batch, void *out, uint32_t cols, uint32_t rows, hipStream_t s) {
+    size_t pf = 0, nc = 0;
+    gemv_mt_workspace_need(type, layout, cols, rows, up != nullptr, batch, xh, &pf, &nc);
+    if (int rc = ensure_ws(ctx, pf, nc)) return rc;
+    const hipError_t e = launch_gemv_mt(type, layout, static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(up),
+                                        x, xh, batch, out, cols, rows, ctx->ws, s);
+    return e == hipSuccess ? NS_OK : hip_fail(e, fn);
+}
+
 int gemm(ns_ctx *ctx, const char *fn, int type, int layout, int acc, const void *w, const void *up,
          const uint16_t *x, void *out, uint32_t cols, uint32_t rows, uint32_t batch, hipStream_t s) {
     if (layout == ROW_MAJOR)
@@ -129,6 +140,10 @@ extern "C" int ns_matmul(ns_ctx *ctx, const void *w, int type, int layout, uint3
     if (int rc = check_tensor("ns_matmul", w, type, layout, cols, rows)) return rc;
     if (!in || !out || batch == 0) return fail(NS_ERR_ARG, "ns_matmul: null input/output or zero batch");
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    // mm:269-275: batch 2-4 -> the small-batch kernels (fp32 or fp16 input); batch > 4 with
+    // fp16 input -> the MMA (prefill) GEMM
+    if (batch >= 2 && batch <= 4)
+        return gemv_mt(ctx, "ns_matmul", type, layout, w, nullptr, in, half_input != 0, batch, out, cols, rows, s);
     if (half_input && batch > 1)
         return gemm(ctx, "ns_matmul", type, layout, ACC_FP32, w, nullptr, static_cast<const uint16_t *>(in), out,
                     cols, rows, batch, s);
@@ -151,6 +166,18 @@ extern "C" int ns_gate_up_geglu_decode(ns_ctx *ctx, const void *wg, const void *
                 static_cast<hipStream_t>(stream));
 }
 
+extern "C" int ns_gate_up_geglu(ns_ctx *ctx, const void *wg, const void *wu, int layout, uint32_t cols,
+                                uint32_t rows, uint32_t batch, const uint16_t *x, uint16_t *h, void *stream) {
+    if (!ctx) return fail(NS_ERR_ARG, "ns_gate_up_geglu: null context");
+    if (int rc = check_tensor("ns_gate_up_geglu", wg, Q4_K, layout, cols, rows)) return rc;
+    if (int rc = check_tensor("ns_gate_up_geglu", wu, Q4_K, layout, cols, rows)) return rc;
+    if (!x || !h || batch == 0) return fail(NS_ERR_ARG, "ns_gate_up_geglu: null input/output or zero batch");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    // mm:282: batch <= 4 -> the small-batch pair kernel; larger batches -> the prefill GEMM (FP32 mode)
+    if (batch <= 4) return gemv_mt(ctx, "ns_gate_up_geglu", Q4_K, layout, wg, wu, x, true, batch, h, cols, rows, s);
+    return gemm(ctx, "ns_gate_up_geglu", Q4_K, layout, ACC_FP32, wg, wu, x, h, cols, rows, batch, s);
+}
+
 extern "C" int ns_gate_up_geglu_rm32(ns_ctx *ctx, const void *wg, const void *wu, int layout, uint32_t cols,
                                      uint32_t rows, uint32_t batch, const uint16_t *x, uint16_t *h, int fast_swa,
                                      void *stream) {
@@ -165,7 +192,7 @@ extern "C" int ns_gate_up_geglu_rm32(ns_ctx *ctx, const void *wg, const void *wu
 extern "C" int ns_ffn_down(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, uint32_t rows,
                            uint32_t batch, const void *in, int half_input, int fast_swa, float *out, void *stream) {
     if (!ctx) return fail(NS_ERR_ARG, "ns_ffn_down: null context");
-    if (half_input && batch > 1) {
+    if (half_input && batch > 4) {  // mm:289; batches up to 4 take matmul's small-batch kernels
         if (int rc = check_tensor("ns_ffn_down", w, type, layout, cols, rows)) return rc;
         if (!in || !out) return fail(NS_ERR_ARG, "ns_ffn_down: null input/output");
         return gemm(ctx, "ns_ffn_down", type, layout, fast_swa ? ACC_FP16 : ACC_FP32, w, nullptr,

@@ -190,6 +190,148 @@ __device__ __forceinline__ float q6_dot(const u32x4 (&c)[kQ6Chunks], uint32_t db
     return d * s;
 }
 
+// ---- several tokens (the batch 2-4 regime) -------------------------------------
+//
+// The block is unpacked once and multiplies NT token vectors.  Per token the FMA
+// order is that of q4_dot / q6_dot.  x is fp32 or fp16 (XH); an fp16 x value
+// feeds the mixed-precision FMA directly, as the weight does.
+template <bool XH>
+__device__ __forceinline__ float xval(const void *__restrict__ xb, uint32_t i) {
+    if constexpr (XH) return float(reinterpret_cast<const _Float16 *>(xb)[i]);
+    else return reinterpret_cast<const float *>(xb)[i];
+}
+
+template <int N, int NT, bool XH>
+__device__ __forceinline__ void q4_dot_mt(const u32x4 (&c)[N][kQ4Chunks], const void *const (&xb)[NT],
+                                          const float (&xs)[NT][8], float (&res)[NT][N]) {
+    float A[NT][N][8];
+#pragma unroll
+    for (int k = 0; k < NT; ++k)
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+#pragma unroll
+            for (int g = 0; g < 8; ++g) A[k][n][g] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int p = j >> 1, l0 = 16 * (j & 1);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t il = 64 * p + l0 + 4 * t, ih = il + 32;  // groups 2p, 2p+1
+#pragma unroll
+            for (int n = 0; n < N; ++n) {
+                const uint32_t wv = comp(c[n][1 + j], t), w8 = wv >> 8;
+                const uint32_t lo0 = wv & 0x000F000Fu, hi0 = wv & 0x00F000F0u;
+                const uint32_t lo1 = w8 & 0x000F000Fu, hi1 = w8 & 0x00F000F0u;
+#pragma unroll
+                for (int k = 0; k < NT; ++k) {
+                    float a = A[k][n][2 * p], h = A[k][n][2 * p + 1];
+                    a = __builtin_fmaf(lo_half(lo0), xval<XH>(xb[k], il + 0), a);
+                    a = __builtin_fmaf(lo_half(lo1), xval<XH>(xb[k], il + 1), a);
+                    a = __builtin_fmaf(hi_half(lo0), xval<XH>(xb[k], il + 2), a);
+                    a = __builtin_fmaf(hi_half(lo1), xval<XH>(xb[k], il + 3), a);
+                    h = __builtin_fmaf(lo_half(hi0), xval<XH>(xb[k], ih + 0), h);
+                    h = __builtin_fmaf(lo_half(hi1), xval<XH>(xb[k], ih + 1), h);
+                    h = __builtin_fmaf(hi_half(hi0), xval<XH>(xb[k], ih + 2), h);
+                    h = __builtin_fmaf(hi_half(hi1), xval<XH>(xb[k], ih + 3), h);
+                    A[k][n][2 * p] = a;
+                    A[k][n][2 * p + 1] = h;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+        const float d = lo_half(c[n][0].x), dmin = hi_half(c[n][0].x);
+        const Q4Scales s = q4_scales(c[n][0].y, c[n][0].z, c[n][0].w);
+#pragma unroll
+        for (int k = 0; k < NT; ++k) {
+            float sq = 0.f, sm = 0.f;
+#pragma unroll
+            for (int g = 0; g < 8; ++g) {
+                const float f = (g & 1) ? 1048576.0f : 16777216.0f;
+                sq = __builtin_fmaf(float(q4_sc(s, g)) * f, A[k][n][g], sq);
+                sm = __builtin_fmaf(float(q4_m(s, g)), xs[k][g], sm);
+            }
+            res[k][n] = d * sq - dmin * sm;
+        }
+    }
+}
+
+template <int NT, bool XH>
+__device__ __forceinline__ void q6_dot_mt(const u32x4 (&c)[kQ6Chunks], uint32_t dbits, const void *const (&xb)[NT],
+                                          const float (&xs)[NT][16], float (&res)[NT]) {
+    const float d = lo_half(dbits);
+    float A[NT][16];
+#pragma unroll
+    for (int k = 0; k < NT; ++k)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) A[k][i] = 0.f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t a = comp(c[4 * h + t], u), b = comp(c[4 * h + 2 + t], u);
+                const uint32_t hq = comp(c[8 + 2 * h + t], u);
+                const uint32_t i0 = 128 * h + 16 * t + 4 * u;
+#pragma unroll
+                for (int odd = 0; odd < 2; ++odd) {
+                    const uint32_t aa = odd ? a >> 8 : a, bb = odd ? b >> 8 : b;
+                    const uint32_t h4 = odd ? hq >> 4 : hq << 4, h2 = odd ? hq >> 6 : hq << 2;
+                    const uint32_t e0 = (aa & 0x000F000Fu) | (h4 & 0x00300030u);
+                    const uint32_t e2 = (aa & 0x00F000F0u) | (h4 & 0x03000300u);
+                    const uint32_t e1 = (bb & 0x000F000Fu) | (h2 & 0x00300030u);
+                    const uint32_t e3 = (bb & 0x00F000F0u) | (h2 & 0x03000300u);
+                    const uint32_t io = i0 + odd;  // elements l+odd (lo half) and l+odd+2 (hi half)
+#pragma unroll
+                    for (int k = 0; k < NT; ++k) {
+                        float &g0 = A[k][8 * h + 0 + t], &g1 = A[k][8 * h + 2 + t], &g2 = A[k][8 * h + 4 + t],
+                              &g3 = A[k][8 * h + 6 + t];
+                        g0 = __builtin_fmaf(lo_half(e0), xval<XH>(xb[k], io + 0), g0);
+                        g0 = __builtin_fmaf(hi_half(e0), xval<XH>(xb[k], io + 2), g0);
+                        g1 = __builtin_fmaf(lo_half(e1), xval<XH>(xb[k], io + 32), g1);
+                        g1 = __builtin_fmaf(hi_half(e1), xval<XH>(xb[k], io + 34), g1);
+                        g2 = __builtin_fmaf(lo_half(e2), xval<XH>(xb[k], io + 64), g2);
+                        g2 = __builtin_fmaf(hi_half(e2), xval<XH>(xb[k], io + 66), g2);
+                        g3 = __builtin_fmaf(lo_half(e3), xval<XH>(xb[k], io + 96), g3);
+                        g3 = __builtin_fmaf(hi_half(e3), xval<XH>(xb[k], io + 98), g3);
+                    }
+                }
+            }
+#pragma unroll
+    for (int k = 0; k < NT; ++k) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float f = ((i >> 1) & 3) >= 2 ? 1048576.0f : 16777216.0f;
+            const float sc = float(int8_t(byte_of(comp(c[12], i >> 2), i & 3)));
+            s = __builtin_fmaf(sc, __builtin_fmaf(A[k][i], f, -32.0f * xs[k][i]), s);
+        }
+        res[k] = d * s;
+    }
+}
+
+// group_sums for fp32 or fp16 x (each lane adds 4 values in fp32).
+template <int GROUP, bool XH>
+__device__ __forceinline__ void group_sums_x(const void *__restrict__ xb, uint32_t lane, float *xs) {
+    float s;
+    if constexpr (XH) {
+        typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+        const half4_t v = reinterpret_cast<const half4_t *>(xb)[lane];
+        s = (float(v.x) + float(v.y)) + (float(v.z) + float(v.w));
+    } else {
+        const float4 v = reinterpret_cast<const float4 *>(xb)[lane];
+        s = (v.x + v.y) + (v.z + v.w);
+    }
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    if constexpr (GROUP == 32) s += __shfl_xor(s, 4);
+#pragma unroll
+    for (int g = 0; g < 256 / GROUP; ++g)
+        xs[g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), g * (GROUP / 4)));
+}
+
 // Sums of x over the block's groups of 32 (Q4_K, 8 values) or 16 (Q6_K, 16
 // values), returned wave-uniform.  Each lane adds 4 values; the groups are
 // completed with cross-lane exchanges and read back with readlane.
@@ -392,6 +534,213 @@ __global__ __launch_bounds__(max_wg_waves(TYPE, PAIR) * 64) void gemv_kernel(
     }
 }
 
+// NT tokens: out[t][r] for t < batch (x[t] at x + t*cols; tokens past batch
+// repeat the last one and are not written).  PAIR with OUTH writes fp16 h
+// (gemma_q4k_gate_up_geglu_mm_f16, metal:102-107); plain writes fp32
+// (gemma_q4k/q6k_mm_fast[_f16], metal:125-177).  Same work split as gemv_kernel.
+constexpr uint32_t max_wg_waves_mt(int type, bool pair, int nt) { return (type == Q4_K && !pair && nt <= 2) ? 12 : 8; }
+
+template <int TYPE, int LAYOUT, bool PAIR, int NT, bool XH, bool OUTH>
+__global__ __launch_bounds__(max_wg_waves_mt(TYPE, PAIR, NT) * 64) void gemv_mt_kernel(
+    const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, const void *__restrict__ x, uint32_t batch,
+    void *__restrict__ out, uint32_t rows, uint32_t nb, uint32_t nslabs, float *__restrict__ partial,
+    uint32_t *__restrict__ counters) {
+    constexpr uint32_t kP = (PAIR ? 2 : 1) * NT;  // values per row: plane-major (gate 0..NT-1, up 0..NT-1)
+    constexpr uint32_t kMaxW = max_wg_waves_mt(TYPE, PAIR, NT);
+    constexpr uint32_t kXBytes = XH ? 2 : 4;
+    // The next unit's weights are loaded while one is computed, except for the
+    // four-token gate/up pair, whose accumulators leave no registers for them.
+    constexpr bool kPrefetch = !(PAIR && NT == 4);
+    __shared__ float lds_part[kMaxW][2][kP][64];
+    __shared__ uint32_t lds_slab[kMaxW][2];
+    const uint32_t nw = blockDim.x >> 6;
+    const uint32_t cols = nb * kQK;
+
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t G = gridDim.x, g = blockIdx.x, U = nslabs * nb;
+    const Split sp{U / G, U % G};
+    const uint32_t wg0 = sp.first(g), wg1 = sp.first(g + 1), n = wg1 - wg0;
+    const uint32_t i0 = wg0 + wave * n / nw, i1 = wg0 + (wave + 1) * n / nw;
+    const uint8_t *xtok[NT];
+#pragma unroll
+    for (int k = 0; k < NT; ++k)
+        xtok[k] = static_cast<const uint8_t *>(x) + size_t(__builtin_elementwise_min(uint32_t(k), batch - 1)) * cols * kXBytes;
+
+    if (lane < 2) lds_slab[wave][lane] = ~0u;
+    float acc[kP];
+#pragma unroll
+    for (int k = 0; k < int(kP); ++k) acc[k] = 0.f;
+    uint32_t slab = i0 / nb, b = i0 - slab * nb, seg_b0 = b, segi = 0;
+
+    auto store_out = [&](uint32_t row, const float (&v)[kP]) {
+#pragma unroll
+        for (int k = 0; k < NT; ++k) {
+            if (uint32_t(k) >= batch) break;
+            if constexpr (PAIR) {
+                const float hv = gelu_tanh(v[k]) * v[NT + k];
+                if constexpr (OUTH) static_cast<_Float16 *>(out)[size_t(k) * rows + row] = _Float16(hv);
+                else static_cast<float *>(out)[size_t(k) * rows + row] = hv;
+            } else {
+                static_cast<float *>(out)[size_t(k) * rows + row] = v[k];
+            }
+        }
+    };
+    auto step_done = [&](uint32_t i) {
+        if (b == nb - 1 || i + 1 == i1) {
+            if (seg_b0 == 0 && b == nb - 1) {
+                const uint32_t row = slab * kRowTile + lane;
+                if (row < rows) store_out(row, acc);
+            } else {
+#pragma unroll
+                for (int k = 0; k < int(kP); ++k) lds_part[wave][segi][k][lane] = acc[k];
+                if (lane == 0) lds_slab[wave][segi] = slab;
+                segi = 1;
+            }
+#pragma unroll
+            for (int k = 0; k < int(kP); ++k) acc[k] = 0.f;
+            seg_b0 = 0;
+        }
+    };
+    auto lrow = [&](uint32_t s) { return __builtin_elementwise_min(s * kRowTile + lane, rows - 1); };
+    auto advance = [&](uint32_t &s, uint32_t &bb) {
+        if (++bb == nb) {
+            bb = 0;
+            ++s;
+        }
+    };
+
+    if (i0 < i1) {
+        if constexpr (TYPE == Q4_K) {
+            constexpr int N = PAIR ? 2 : 1;
+            const uint8_t *wm[2] = {w0, w1};
+            u32x4 c[N][kQ4Chunks];
+            if constexpr (kPrefetch)
+#pragma unroll
+                for (int m = 0; m < N; ++m) q4_load<LAYOUT>(wm[m], lane, lrow(slab), slab, b, nb, c[m]);
+            for (uint32_t i = i0; i < i1; ++i) {
+                uint32_t ns_ = slab, nbk = b;
+                advance(ns_, nbk);
+                u32x4 nx[N][kQ4Chunks];
+                if constexpr (kPrefetch) {
+                    if (i + 1 < i1)
+#pragma unroll
+                        for (int m = 0; m < N; ++m) q4_load<LAYOUT>(wm[m], lane, lrow(ns_), ns_, nbk, nb, nx[m]);
+                } else {
+#pragma unroll
+                    for (int m = 0; m < N; ++m) q4_load<LAYOUT>(wm[m], lane, lrow(slab), slab, b, nb, c[m]);
+                }
+                const void *xb[NT];
+                float xs[NT][8], r[NT][N];
+#pragma unroll
+                for (int k = 0; k < NT; ++k) {
+                    xb[k] = xtok[k] + size_t(b) * kQK * kXBytes;
+                    group_sums_x<32, XH>(xb[k], lane, xs[k]);
+                }
+                q4_dot_mt<N, NT, XH>(c, xb, xs, r);
+#pragma unroll
+                for (int k = 0; k < NT; ++k) {
+                    acc[k] += r[k][0];
+                    if constexpr (PAIR) acc[NT + k] += r[k][N - 1];
+                }
+                step_done(i);
+                slab = ns_;
+                b = nbk;
+                if constexpr (kPrefetch)
+#pragma unroll
+                    for (int m = 0; m < N; ++m)
+#pragma unroll
+                        for (int q = 0; q < int(kQ4Chunks); ++q) c[m][q] = nx[m][q];
+            }
+        } else {
+            u32x4 c0[kQ6Chunks];
+            uint32_t d0 = 0;
+            q6_load<LAYOUT>(w0, lane, lrow(slab), slab, b, nb, c0, d0);
+            for (uint32_t i = i0; i < i1; ++i) {
+                uint32_t ns_ = slab, nbk = b;
+                advance(ns_, nbk);
+                u32x4 n0[kQ6Chunks];
+                uint32_t dn = 0;
+                if (i + 1 < i1) q6_load<LAYOUT>(w0, lane, lrow(ns_), ns_, nbk, nb, n0, dn);
+                const void *xb[NT];
+                float xs[NT][16], r[NT];
+#pragma unroll
+                for (int k = 0; k < NT; ++k) {
+                    xb[k] = xtok[k] + size_t(b) * kQK * kXBytes;
+                    group_sums_x<16, XH>(xb[k], lane, xs[k]);
+                }
+                q6_dot_mt<NT, XH>(c0, d0, xb, xs, r);
+#pragma unroll
+                for (int k = 0; k < NT; ++k) acc[k] += r[k];
+                step_done(i);
+                slab = ns_;
+                b = nbk;
+#pragma unroll
+                for (int q = 0; q < int(kQ6Chunks); ++q) c0[q] = n0[q];
+                d0 = dn;
+            }
+        }
+    }
+    if (n == 0) return;
+    const uint32_t s_lo = wg0 / nb, s_hi = (wg1 - 1) / nb;
+    __syncthreads();
+    for (uint32_t s = s_lo + wave; s <= s_hi; s += nw) {
+        float r[kP];
+#pragma unroll
+        for (int k = 0; k < int(kP); ++k) r[k] = 0.f;
+        bool any = false;
+        for (uint32_t v = 0; v < nw; ++v)
+#pragma unroll
+            for (uint32_t q = 0; q < 2; ++q)
+                if (lds_slab[v][q] == s) {
+#pragma unroll
+                    for (int k = 0; k < int(kP); ++k) r[k] += lds_part[v][q][k][lane];
+                    any = true;
+                }
+        if (!any) continue;  // whole slab, already written
+        const uint32_t row = s * kRowTile + lane;
+        const bool cut = s * nb < wg0 || (s + 1) * nb > wg1;
+        if (cut) {
+            // hand-off between workgroups as in gemv_kernel, kP values per row
+            const uint32_t slot = s == s_lo ? 0u : 1u;
+            float *dst = partial + (size_t(g) * 2 + slot) * (kP * 64);
+#pragma unroll
+            for (int k = 0; k < int(kP); ++k)
+                __hip_atomic_store(&dst[k * 64 + lane], r[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_s_waitcnt(0);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            const uint32_t gf = sp.owner(s * nb), gl = sp.owner(s * nb + nb - 1);
+            uint32_t prev = 0;
+            if (lane == 0) prev = __hip_atomic_fetch_add(&counters[s], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            prev = __builtin_amdgcn_readfirstlane(__shfl(prev, 0));
+            if (prev != gl - gf) continue;
+#pragma unroll
+            for (int k = 0; k < int(kP); ++k) r[k] = 0.f;
+            // parts of workgroups gf..gl, 4 at a time (kP values each), added in order
+            for (uint32_t h0 = gf; h0 <= gl; h0 += 4) {
+                float v[4][kP];
+#pragma unroll
+                for (uint32_t j = 0; j < 4; ++j) {
+                    const uint32_t h = __builtin_elementwise_min(h0 + j, gl);
+                    const uint32_t si = sp.first(h) < s * nb ? 1u : 0u;
+                    const float *pp = partial + (size_t(h) * 2 + si) * (kP * 64);
+#pragma unroll
+                    for (int k = 0; k < int(kP); ++k)
+                        v[j][k] = __hip_atomic_load(&pp[k * 64 + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+#pragma unroll
+                for (uint32_t j = 0; j < 4; ++j)
+                    if (h0 + j <= gl)
+#pragma unroll
+                        for (int k = 0; k < int(kP); ++k) r[k] += v[j][k];
+            }
+            if (lane == 0) __hip_atomic_store(&counters[s], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (row < rows) store_out(row, r);
+    }
+}
+
 int env_int(const char *name, int dflt) {
     const char *v = getenv(name);
     return v && *v ? atoi(v) : dflt;
@@ -495,6 +844,52 @@ hipError_t launch_typed(int layout, const uint8_t *w, const uint8_t *up, const f
     return hipGetLastError();
 }
 
+// ---- batch 2-4: one instance per (type, layout, pair, NT, fp16 x) -------------
+template <int TYPE, int LAYOUT, bool PAIR, int NT, bool XH>
+struct Mt {
+    static constexpr auto kernel() { return &gemv_mt_kernel<TYPE, LAYOUT, PAIR, NT, XH, PAIR>; }
+    static GemvPlan plan(uint32_t cols, uint32_t rows) {
+        static int cache[64] = {};  // resident waves per CU, per device
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        int &w = cache[dev & 63];
+        if (w == 0) {
+            int wgs = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&wgs, kernel(), kWgWaves * 64, 0) != hipSuccess || wgs <= 0)
+                wgs = 2;
+            w = wgs * kWgWaves;
+        }
+        const uint32_t cus = uint32_t(device_shape().cus);
+        return plan_gemv(cols, rows, w * int(cus), max_wg_waves_mt(TYPE, PAIR, NT), cus);
+    }
+};
+
+template <int TYPE, bool PAIR, int NT, bool XH, class Fn>
+auto mt_by_layout(int layout, Fn &&fn) {
+    if (layout == CDNA4) return fn(Mt<TYPE, CDNA4, PAIR, NT, XH>{});
+    if (layout == NSMFFN) return fn(Mt<TYPE, NSMFFN, PAIR, NT, XH>{});
+    return fn(Mt<TYPE, ROW_MAJOR, PAIR, NT, XH>{});
+}
+template <int TYPE, bool PAIR, bool XH, class Fn>
+auto mt_by_nt(uint32_t nt, int layout, Fn &&fn) {
+    if constexpr (XH)
+        return nt == 2 ? mt_by_layout<TYPE, PAIR, 2, XH>(layout, fn) : mt_by_layout<TYPE, PAIR, 4, XH>(layout, fn);
+    else
+        return mt_by_layout<TYPE, PAIR, 4, XH>(layout, fn);
+}
+// The gate/up pair takes fp16 x and writes fp16 h (the reference's only small-batch pair kernel).
+template <class Fn>
+auto dispatch_mt(int type, int layout, bool pair, uint32_t nt, bool xh, Fn &&fn) {
+    if (pair) return mt_by_nt<Q4_K, true, true>(nt, layout, fn);
+    if (type == Q4_K) return xh ? mt_by_nt<Q4_K, false, true>(nt, layout, fn) : mt_by_nt<Q4_K, false, false>(nt, layout, fn);
+    return xh ? mt_by_nt<Q6_K, false, true>(nt, layout, fn) : mt_by_nt<Q6_K, false, false>(nt, layout, fn);
+}
+
+// Tokens per kernel instance.  fp32 x takes the four-token instance for every
+// batch: two tokens of fp32 x do not fit the scalar registers the instance keeps
+// x in, and the spilled instance is slower than the four-token one (MI355X).
+uint32_t mt_tokens(uint32_t batch, bool xh) { return xh && batch <= 2 ? 2u : 4u; }
+
 }  // namespace
 
 void gemv_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, bool pair, size_t *partial_floats,
@@ -510,6 +905,27 @@ hipError_t launch_gemv(int type, int layout, const uint8_t *w, const uint8_t *up
     if (up) return launch_typed<Q4_K, true>(layout, w, up, x, out, cols, rows, ws, stream);
     if (type == Q4_K) return launch_typed<Q4_K, false>(layout, w, nullptr, x, out, cols, rows, ws, stream);
     return launch_typed<Q6_K, false>(layout, w, nullptr, x, out, cols, rows, ws, stream);
+}
+
+void gemv_mt_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, bool pair, uint32_t batch, bool xh,
+                            size_t *partial_floats, size_t *counters) {
+    const uint32_t nt = mt_tokens(batch, xh);
+    const GemvPlan p = dispatch_mt(type, layout, pair, nt, xh, [&](auto m) { return decltype(m)::plan(cols, rows); });
+    *partial_floats = size_t(p.G) * 2 * 64 * (pair ? 2 : 1) * nt;
+    *counters = p.nslabs;
+}
+
+hipError_t launch_gemv_mt(int type, int layout, const uint8_t *w, const uint8_t *up, const void *x, bool xh,
+                          uint32_t batch, void *out, uint32_t cols, uint32_t rows, const Workspace &ws,
+                          hipStream_t stream) {
+    const bool pair = up != nullptr;
+    return dispatch_mt(type, layout, pair, mt_tokens(batch, xh), xh, [&](auto m) {
+        using M = decltype(m);
+        const GemvPlan p = M::plan(cols, rows);
+        M::kernel()<<<dim3(p.G), dim3(p.W * 64), 0, stream>>>(w, up, x, batch, out, rows, cols / kQK, p.nslabs,
+                                                               ws.partial, ws.counters);
+        return hipGetLastError();
+    });
 }
 
 }  // namespace ns

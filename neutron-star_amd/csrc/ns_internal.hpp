@@ -32,6 +32,15 @@ hipError_t launch_gemv(int type, int layout, const uint8_t *w, const uint8_t *up
 void gemv_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, bool pair, size_t *partial_floats,
                          size_t *counters);
 
+// Batch 2-4 (the reference's mm_fast / gate_up_geglu_mm regime): the weights
+// are streamed once for all tokens.  x: [batch][cols], fp16 (xh) or fp32;
+// out: [batch][rows], fp32, or fp16 h for the gate/up pair (up non-null, fp16 x).
+hipError_t launch_gemv_mt(int type, int layout, const uint8_t *w, const uint8_t *up, const void *x, bool xh,
+                          uint32_t batch, void *out, uint32_t cols, uint32_t rows, const Workspace &ws,
+                          hipStream_t stream);
+void gemv_mt_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, bool pair, uint32_t batch, bool xh,
+                            size_t *partial_floats, size_t *counters);
+
 // Workspace the prefill GEMM needs: Q4_K group sums of x, split-K parts, tile counters.
 void gemm_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, uint32_t batch, bool pair,
                          size_t *floats, size_t *counters);

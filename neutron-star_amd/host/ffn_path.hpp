@@ -118,6 +118,14 @@ public:
         check(ns_matmul(ctx_, w_.data(w), int(w.type), int(w_.layout(w)), cols(w), rows(w), batch, in,
                         half_input ? 1 : 0, out, e));
     }
+    // mm:281: gate/up + GeGLU, fp16 in, fp16 out; batch <= 4 (MTP verification) streams
+    // the weights once for every token.
+    void gate_up_geglu(hipStream_t e, const Tensor &gate, const Tensor &up, const uint16_t *in, uint16_t *out,
+                       uint32_t batch) const {
+        same_shape(gate, up);
+        check(ns_gate_up_geglu(ctx_, w_.data(gate), w_.data(up), int(w_.layout(gate)), cols(gate), rows(gate), batch,
+                               in, out, e));
+    }
     // mm:288: prefill gate/up + GeGLU, fp16 in, fp16 out; fast_swa selects the FP16 mode.
     void gate_up_geglu_rm32(hipStream_t e, const Tensor &gate, const Tensor &up, const uint16_t *in, uint16_t *out,
                             uint32_t batch, bool fast_swa) const {

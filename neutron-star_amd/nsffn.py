@@ -62,6 +62,7 @@ def lib():
             "ns_matmul": [vp, vp, i32, i32, u32, u32, u32, vp, i32, vp, vp],
             "ns_gate_up_geglu_decode": [vp, vp, vp, i32, u32, u32, vp, vp, vp],
             "ns_gate_up_geglu_rm32": [vp, vp, vp, i32, u32, u32, u32, vp, vp, i32, vp],
+            "ns_gate_up_geglu": [vp, vp, vp, i32, u32, u32, u32, vp, vp, vp],
             "ns_ffn_down": [vp, vp, i32, i32, u32, u32, u32, vp, i32, i32, vp, vp],
             "ns_dequant": [vp, vp, i32, i32, u32, u32, u32, u32, vp, vp, vp],
             "ns_standardize": [vp, vp, u32, u32, vp, i32, vp],
@@ -231,6 +232,11 @@ class Context:
     def gate_up_geglu_decode(self, wg, wu, layout, cols, rows, x, h, stream=None):
         check(lib().ns_gate_up_geglu_decode(self.handle, _ptr(wg), _ptr(wu), layout, cols, rows,
                                             _ptr(x), _ptr(h), _stream(stream)))
+
+    def gate_up_geglu(self, wg, wu, layout, cols, rows, batch, x, h, stream=None):
+        """gate_up_geglu (mm:281): fp16 x and h; batch <= 4 streams the weights once."""
+        check(lib().ns_gate_up_geglu(self.handle, _ptr(wg), _ptr(wu), layout, cols, rows, batch,
+                                     _ptr(x), _ptr(h), _stream(stream)))
 
     def gate_up_geglu_rm32(self, wg, wu, layout, cols, rows, batch, x, h, fast_swa, stream=None):
         check(lib().ns_gate_up_geglu_rm32(self.handle, _ptr(wg), _ptr(wu), layout, cols, rows, batch,

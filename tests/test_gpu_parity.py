@@ -190,6 +190,10 @@ def test_prefill_down_small(ctx, cols, rows, batch, qtype, acc, layout):
     torch.cuda.synchronize()
     got = y.cpu().numpy()
     ref32 = O.gemm(qtype, O.ROW_MAJOR, hw, cols, rows, batch, x, 0)
+    if batch <= 4:
+        # mm:289: fp16 input at batch <= 4 goes to matmul's small-batch kernels, FP32 in both modes
+        assert rel_err(got, ref32) <= TOL32
+        return
     assert rel_err(got, ref32) <= (TOL32 if acc == N.ACC_FP32 else TOL16)
     if acc == N.ACC_FP16:
         assert not np.any(got.view(np.uint32) & 0x1FFF)  # fp16 precision: 11 significant bits
