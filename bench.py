@@ -12,10 +12,13 @@ Also reported under "extra":
   config 3  prefill FFN block at batch 1024, both accumulation modes, tokens/s;
   config 4  48-layer FFN stack (Q4_K_M mix), prefill at batch 1024 then 64 decode
             steps each ending in the lm-head GEMV; the decode step also replayed
-            from a HIP graph.
+            from a HIP graph;
+  batch 2/4 the MTP-verification regime (mm:273, :282): lm-head (fp32 x), gate/up
+            pair and Q6_K down (fp16 x), weights streamed once for all tokens;
+            beside it, the lm-head as one GEMV per token.
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--only all|headline|lmhead|prefill|stack]
+                       [--only all|headline|lmhead|prefill|stack|smallbatch]
   --only lmhead runs just the lm-head GEMV (K launches) and a 256 MiB device copy
   of known size: the driver for the rocprofv3 --pmc traffic runs.
 """
@@ -51,6 +54,45 @@ BYTES_Q6_DOWN = qbytes(Q6, D, F) + 4 * F + 4 * D                 # 48,460,800
 BYTES_Q6_LMHEAD = qbytes(Q6, V, D) + 4 * D + 4 * V               # 826,817,536
 BYTES_FFN_LAYER = 2 * qbytes(Q4, F, D) + qbytes(Q6, D, F)        # 114,739,200 (weights)
 FLOPS_PREFILL_LAYER = 2 * B * F * D * 2 + 2 * B * D * F          # 362,387,865,600
+
+
+class TimingEvent:
+    """A HIP event created with hipEventDisableSystemFence (hip_runtime_api.h): recording it
+    skips the system-scope cache write-back and invalidation of a default event, which on
+    this box leaves the stream idle for ~6 us and so would distort the kernels it brackets.
+    Bound through the HIP runtime the process already loaded (torch's)."""
+    _lib = None
+
+    @classmethod
+    def lib(cls):
+        if cls._lib is None:
+            import ctypes
+            path = next(l.split()[-1] for l in open("/proc/self/maps") if "libamdhip64" in l)
+            cls._lib = ctypes.CDLL(path)
+        return cls._lib
+
+    def __init__(self):
+        import ctypes
+        self.ev = ctypes.c_void_p()
+        if self.lib().hipEventCreateWithFlags(ctypes.byref(self.ev), 0x20000000) != 0:
+            raise RuntimeError("hipEventCreateWithFlags failed")
+
+    def record(self, stream):
+        import ctypes
+        if self.lib().hipEventRecord(self.ev, ctypes.c_void_p(stream.cuda_stream)) != 0:
+            raise RuntimeError("hipEventRecord failed")
+
+    def elapsed_ms(self, end):
+        import ctypes
+        ms = ctypes.c_float()
+        self.lib().hipEventSynchronize(end.ev)
+        if self.lib().hipEventElapsedTime(ctypes.byref(ms), self.ev, end.ev) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def __del__(self):
+        if self._lib is not None and self.ev:
+            self._lib.hipEventDestroy(self.ev)
 
 
 def down_type(layer):
@@ -152,10 +194,12 @@ class Bench:
             if ev is not None:
                 ev[1].record(self.stream)
 
+        # The lm-head's launch duration is timed inside the timed steps with events
+        # that carry no system-scope fence (TimingEvent), so they do not stall the stream.
         for i in range(args.warmup):
             step(i)
         torch.cuda.synchronize()
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+        evs = [(TimingEvent(), TimingEvent()) for _ in range(args.steps)]
         t0 = time.perf_counter()
         for i in range(args.steps):
             step(i, evs[i])
@@ -163,7 +207,7 @@ class Bench:
         wall = time.perf_counter() - t0
         self.ms_per_step = 1e3 * wall / args.steps
         self.value = (BYTES_Q6_DOWN + BYTES_Q6_LMHEAD) / (wall / args.steps) / 1e9
-        lm_ms = float(np.mean([a.elapsed_time(b) for a, b in evs]))
+        lm_ms = float(np.mean([a.elapsed_ms(b) for a, b in evs]))
         self.lm_gbs = BYTES_Q6_LMHEAD / (lm_ms * 1e-3) / 1e9
         log(f"config1: {self.ms_per_step:.4f} ms/step, {self.value:.1f} GB/s; lm-head {lm_ms * 1e3:.1f} us "
             f"= {self.lm_gbs:.1f} GB/s")
@@ -240,6 +284,38 @@ class Bench:
                                f"cfg3_{name}_gate_up_ms": round(gu_ms, 4), f"cfg3_{name}_down_ms": round(dn_ms, 4)})
             log(f"config3 {name}: {p_ms:.3f} ms/block = {B / (p_ms * 1e-3):.0f} tok/s, {tf:.0f} TFLOP/s "
                 f"(gate/up {gu_ms:.3f} ms, down {dn_ms:.3f} ms)")
+
+    # -- batch 2-4 (MTP verification) ----------------------------------------------------
+    def smallbatch(self):
+        N, torch, ctx = self.N, self.torch, self.ctx
+        if not hasattr(self, "lm"):
+            self.lm = self.weights(Q6, 0x1B, V, D)
+        # four copies of the FFN matrices (460 MB) so the Infinity Cache cannot hold them
+        gs = [self.weights(Q4, 0xA0 + i, F, D) for i in range(4)]
+        us = [self.weights(Q4, 0xA4 + i, F, D) for i in range(4)]
+        ds = [self.weights(Q6, 0xA8 + i, D, F) for i in range(4)]
+        lm_w, gu_w, dn_w = qbytes(Q6, V, D), 2 * qbytes(Q4, F, D), qbytes(Q6, D, F)
+        for nb in (2, 4):
+            xf = self.f32(0xB0 + nb, nb * D).reshape(nb, D)
+            xh = self.f16(0xB2 + nb, nb * D).reshape(nb, D)
+            hf = self.f16(0xB4 + nb, nb * F).reshape(nb, F)
+            lg = torch.empty((nb, V), dtype=torch.float32, device="cuda")
+            hh = torch.empty((nb, F), dtype=torch.int16, device="cuda")
+            y = torch.empty((nb, D), dtype=torch.float32, device="cuda")
+            lm_ms = self.timed(lambda i: ctx.matmul(self.lm, Q6, N.CDNA4, D, V, nb, xf, lg), 10)
+            gu_ms = self.timed(lambda i: ctx.gate_up_geglu(gs[i % 4], us[i % 4], N.CDNA4, D, F, nb, xh, hh), 32)
+            dn_ms = self.timed(lambda i: ctx.ffn_down(ds[i % 4], Q6, N.CDNA4, F, D, nb, hf, y, True, False), 32)
+            r = {"lm_head": (lm_ms, lm_w + nb * 4 * (D + V)), "gate_up": (gu_ms, gu_w + nb * 2 * (D + F)),
+                 "down": (dn_ms, dn_w + nb * (2 * F + 4 * D))}
+            for k, (ms, nbytes) in r.items():
+                self.extra[f"sb{nb}_{k}_us"] = round(ms * 1e3, 2)
+                self.extra[f"sb{nb}_{k}_GBps"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+            if nb == 4:
+                pt_ms = self.timed(lambda i: [ctx.matmul(self.lm, Q6, N.CDNA4, D, V, 1, xf[t], lg[t])
+                                              for t in range(nb)], 5)
+                self.extra["sb4_lm_head_per_token_gemvs_us"] = round(pt_ms * 1e3, 2)
+            log(f"batch {nb}: lm-head {lm_ms * 1e3:.1f} us, gate/up {gu_ms * 1e3:.1f} us, down {dn_ms * 1e3:.1f} us"
+                + (f" (lm-head as {nb} GEMVs: {pt_ms * 1e3:.1f} us)" if nb == 4 else ""))
 
     # -- configs 2 and 4: the 48-layer stack -------------------------------------------
     def stack(self):
@@ -356,7 +432,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--quick", action="store_true", help="same as --only headline")
-    ap.add_argument("--only", default="all", choices=["all", "headline", "lmhead", "prefill", "stack"])
+    ap.add_argument("--only", default="all", choices=["all", "headline", "lmhead", "prefill", "stack", "smallbatch"])
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {args.gpus}); how the path would shard is described "
@@ -375,10 +451,15 @@ def main():
         bench.stack()
         print(json.dumps({"extra": bench.extra}), flush=True)
         return
+    if only == "smallbatch":
+        bench.smallbatch()
+        print(json.dumps({"extra": bench.extra}), flush=True)
+        return
     bench.config1()
     if only == "all":
         bench.config0()
         bench.config3()
+        bench.smallbatch()
         bench.stack()
     cpu = None if args.no_cpu else bench.cpu_baseline()
     out = {
