@@ -14,9 +14,9 @@
 // MFMA products with fp16 x are exact, and the per-row factors are applied once
 // per super-block on the accumulators:
 //   Y += d * acc_sb  [- dmin * sum_g m_g * S_g(x)]            (S_g = sum of x over group g)
-// The Q4_K min term is one extra MFMA per super-block whose K runs over the 8
+// The Q4_K min term is two extra MFMAs per super-block whose K runs over the 8
 // groups: A = the group sums of x split into fp16 hi + lo (k 0..7 and 8..15),
-// B = m_g.  This keeps the FP32 mode at fp32 accuracy (a plain fp16 copy of the
+// B = the min factors, likewise as fp16 hi + lo.  This keeps the FP32 mode at fp32 accuracy (a plain fp16 copy of the
 // dequantised weights would add ~1e-3 relative error by itself) and needs fewer
 // VALU operations per weight than materialising d*sc*q - dmin*m.
 //
@@ -220,10 +220,12 @@ __device__ __forceinline__ void decode(const RawQ6 &r, uint32_t s, uint32_t hh, 
 // The tile holds z*sc*q with z = d/e, i.e. the exact integers sc*q whenever
 // e = d; the rare Q4_K blocks with d < dmin/1024 get z < 1 (rounded in fp16,
 // an error on a term at most ~1e-3 of the block's own min term).  The Q4_K
-// min term -dmin/e * sum_g m_g S_g(x) is one more MFMA accumulating into the
+// min term -dmin/e * sum_g m_g S_g(x) is two more MFMAs accumulating into the
 // same registers: A = the group sums of x split into fp16 hi (k 0..7) and lo
-// (k 8..15), B = fp16(-dmin/e * m_g) (|.| <= 1024*63; rounding it costs < 3e-4
-// of a term that is a few percent of the output).  Entering super-block sb+1
+// (k 8..15); B = b_g = fp16(-dmin/e * m_g) (|.| <= 1024*63) in both halves, then
+// the residues fp16(-dmin/e * m_g - b_g) against the hi sums only.  With b_g
+// alone the min term carried 11 significant bits, which on blocks with d = 0
+// (pure min term) put the gate/up output 1.2e-3 off.  Entering super-block sb+1
 // multiplies the accumulator by e_sb / e_sb+1.
 //
 // Pipeline, per 64-wide k step s (one barrier per step):
@@ -253,7 +255,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     __shared__ __attribute__((aligned(16))) _Float16 Ws[2][TC * LDSW];
     __shared__ __attribute__((aligned(16))) u32x4 Xs[2][TT * 8];
     __shared__ float colE[2][TC];
-    __shared__ __attribute__((aligned(16))) _Float16 colB[2][Q4 ? TC * 8 : 8];
+    // Q4_K min factors per column: 8 fp16 values b_g, then their 8 rounding residues
+    __shared__ __attribute__((aligned(16))) _Float16 colB[2][Q4 ? TC * 16 : 16];
     __shared__ uint32_t last_flag;
 
     const uint32_t tid = threadIdx.x, lane = tid & 63;
@@ -342,12 +345,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
             if constexpr (Q4) {
                 const float f = -hi_half(rw.hdr.x) * re;
                 const Q4Scales sc = q4_scales(rw.hdr.y, rw.hdr.z, rw.hdr.w);
-                u32x4 mv;
+                half8_t bh, bl;
 #pragma unroll
-                for (int g = 0; g < 8; g += 2)
-                    mv[g / 2] = uint32_t(__builtin_bit_cast(uint16_t, _Float16(f * float(q4_m(sc, g))))) |
-                                (uint32_t(__builtin_bit_cast(uint16_t, _Float16(f * float(q4_m(sc, g + 1))))) << 16);
-                *reinterpret_cast<u32x4 *>(&colB[pb][wc * 8]) = mv;
+                for (int g = 0; g < 8; ++g) {
+                    const float v = f * float(q4_m(sc, g));
+                    bh[g] = _Float16(v);
+                    bl[g] = _Float16(v - float(bh[g]));
+                }
+                *reinterpret_cast<half8_t *>(&colB[pb][wc * 16]) = bh;
+                *reinterpret_cast<half8_t *>(&colB[pb][wc * 16 + 8]) = bl;
             }
         }
     };
@@ -432,13 +438,21 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
 
             if constexpr (Q4) {
                 if (j == 3) {  // min term of super-block sb
+                    // b_g in k 0-7 (hi sums) and k 8-15 (lo sums); the residues of b_g in k 0-7
+                    // only (against the hi sums), so the min term keeps ~22 significant bits
 #pragma unroll
                     for (int jj = 0; jj < NJ; ++jj) {
-                        const half8_t bm = *reinterpret_cast<const half8_t *>(&colB[pb][(bcol(jj) + (lane & 31)) * 8]);
+                        const _Float16 *cb = &colB[pb][(bcol(jj) + (lane & 31)) * 16];
+                        const half8_t bm = *reinterpret_cast<const half8_t *>(cb);
+                        half8_t bl = *reinterpret_cast<const half8_t *>(cb + 8);
+                        if (lane >= 32) bl = half8_t{};
 #pragma unroll
                         for (int i = 0; i < MI; ++i)
-                            acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, xsf[i]), bm,
-                                                                                acc[i][jj], 0, 0, 0);
+                            acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                                __builtin_bit_cast(half8_t, xsf[i]), bl,
+                                __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, xsf[i]), bm,
+                                                                       acc[i][jj], 0, 0, 0),
+                                0, 0, 0);
                     }
                 }
             }

@@ -23,8 +23,8 @@
 // 2^-24 for the high nibbles); one packed fp16 multiply by sc * 2^10 (sc * 2^6)
 // gives the fragment values with one rounding of an exact product.  The
 // accumulator holds S / E with E = e * 2^14 per column and super-block; the
-// Q4_K min term is one extra MFMA per super-block over the group sums of x
-// (hi + lo fp16 planes), and entering a new super-block rescales the
+// Q4_K min term is two extra MFMAs per super-block over the group sums of x
+// (hi + lo fp16 planes; the min factors as fp16 hi + lo), and entering a new super-block rescales the
 // accumulator by E_prev / E_cur (FP16 mode: rounds S to fp16 precision there).
 //
 // Tiling: a workgroup of 4 waves computes 128 tokens x 256 B columns; each
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
 
             // super-block entry: E of each column, rescale of the accumulator
             half2_t slo[NJ], shi[NJ];
-            half8_t bmin[NJ];
+            half8_t bmin[NJ], bmin_lo[NJ];
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
                 const Raw &rw = raw[ri][j];
@@ -223,15 +223,20 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
                     Ecur[j] = e * 16384.0f;
                 }
                 if (jstep == 3) {
-                    // min term B fragment: lanes hold m_0..m_7 * (-dmin / E) for k 0-7 (hi sums)
-                    // and again for k 8-15 (lo sums)
+                    // Min term B fragments.  b_g = fp16(m_g * (-dmin / E)) sits in k 0-7 (against
+                    // the hi sums) and again in k 8-15 (against the lo sums); its rounding residue
+                    // fp16(m_g * (-dmin / E) - b_g) is a second fragment, k 0-7 only, against the
+                    // hi sums, so the min term keeps ~22 significant bits (b_g alone: 11).
                     const float f = -dmin * re * 0.00006103515625f;
-                    u32x4 mv;
+                    half8_t bh, bl;
 #pragma unroll
-                    for (int gg = 0; gg < 8; gg += 2)
-                        mv[gg / 2] = uint32_t(__builtin_bit_cast(uint16_t, _Float16(f * float(q4_m(sc, gg))))) |
-                                     (uint32_t(__builtin_bit_cast(uint16_t, _Float16(f * float(q4_m(sc, gg + 1))))) << 16);
-                    bmin[j] = __builtin_bit_cast(half8_t, mv);
+                    for (int gg = 0; gg < 8; ++gg) {
+                        const float v = f * float(q4_m(sc, gg));
+                        bh[gg] = _Float16(v);
+                        bl[gg] = hl == 0 ? _Float16(v - float(bh[gg])) : _Float16(0.0f);
+                    }
+                    bmin[j] = bh;
+                    bmin_lo[j] = bl;
                 }
             }
             // fragments of step s: frag[kk] for kk = 0 (qa lo), 1 (qb lo), 2 (qa hi), 3 (qb hi)
@@ -281,8 +286,11 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
                 for (int i = 0; i < MI; ++i)
 #pragma unroll
                     for (int j = 0; j < NJ; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, xsf[i]), bmin[j],
-                                                                            acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                            __builtin_bit_cast(half8_t, xsf[i]), bmin_lo[j],
+                            __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, xsf[i]), bmin[j],
+                                                                   acc[i][j], 0, 0, 0),
+                            0, 0, 0);
             }
             // x(s+1) must be in LDS for every wave: wait for its DMA (issued one step
             // ago; the loads issued after it -- raw(s+1), x(s+2), raw(s+2) -- may stay
