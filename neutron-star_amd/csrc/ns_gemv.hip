@@ -34,9 +34,12 @@ namespace {
 constexpr uint32_t kWgWaves = 4;   // waves per workgroup of the flattened split
 
 // Largest workgroup (in waves) a kernel instance supports: as many as one CU
-// holds at that kernel's register use (Q4_K ~110 VGPRs: 4 per SIMD; Q6_K
-// ~160: 3; gate/up pair ~190: 2).
-constexpr uint32_t max_wg_waves(int type, bool pair) { return pair ? 8 : (type == Q4_K ? 16 : 12); }
+// holds at that kernel's register use.  With the prefetch buffer (PF): Q4_K
+// ~110 VGPRs, 4 waves per SIMD; Q6_K ~150: 3; gate/up pair ~190: 2.  Without
+// it every instance fits in 128 VGPRs, 4 waves per SIMD.
+constexpr uint32_t max_wg_waves(int type, bool pair, bool pf) {
+    return !pf ? 16 : pair ? 8 : (type == Q4_K ? 16 : 12);
+}
 
 // ---- block loads --------------------------------------------------------
 
@@ -366,13 +369,18 @@ struct Split {
     }
 };
 
-template <int TYPE, int LAYOUT, bool PAIR>
-__global__ __launch_bounds__(max_wg_waves(TYPE, PAIR) * 64) void gemv_kernel(
+// PF: the next unit's weights are loaded while one is computed (the streaming
+// regime, many units per wave).  Without PF a wave loads and computes one unit
+// at a time; that instance needs fewer registers, so a CU holds twice the waves
+// of the gate/up pair, and a grid with one unit per wave issues every load at
+// launch.
+template <int TYPE, int LAYOUT, bool PAIR, bool PF>
+__global__ __launch_bounds__(max_wg_waves(TYPE, PAIR, PF) * 64) void gemv_kernel(
     const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, const float *__restrict__ x,
     float *__restrict__ out, uint32_t rows, uint32_t nb, uint32_t nslabs, float *__restrict__ partial,
     uint32_t *__restrict__ counters) {
     constexpr uint32_t kPlanes = PAIR ? 2 : 1;
-    constexpr uint32_t kMaxW = max_wg_waves(TYPE, PAIR);
+    constexpr uint32_t kMaxW = max_wg_waves(TYPE, PAIR, PF);
     __shared__ float lds_part[kMaxW][2][kPlanes][64];
     __shared__ uint32_t lds_slab[kMaxW][2];
     const uint32_t nw = blockDim.x >> 6;  // waves in this workgroup (<= kMaxW)
@@ -421,50 +429,78 @@ __global__ __launch_bounds__(max_wg_waves(TYPE, PAIR) * 64) void gemv_kernel(
         if constexpr (TYPE == Q4_K) {
             constexpr int N = PAIR ? 2 : 1;
             const uint8_t *wm[2] = {w0, w1};
-            u32x4 c[N][kQ4Chunks];
-#pragma unroll
-            for (int m = 0; m < N; ++m) q4_load<LAYOUT>(wm[m], lane, lrow(slab), slab, b, nb, c[m]);
-            for (uint32_t i = i0; i < i1; ++i) {
-                uint32_t ns_ = slab, nbk = b;
-                advance(ns_, nbk);
-                u32x4 nx[N][kQ4Chunks];
-                if (i + 1 < i1)
-#pragma unroll
-                    for (int m = 0; m < N; ++m) q4_load<LAYOUT>(wm[m], lane, lrow(ns_), ns_, nbk, nb, nx[m]);
+            auto compute = [&](const u32x4(&cc)[N][kQ4Chunks]) {
                 const float *xb = x + size_t(b) * kQK;
                 float xs[8], r[N];
                 group_sums<32>(xb, lane, xs);
-                q4_dot<N>(c, xb, xs, r);
+                q4_dot<N>(cc, xb, xs, r);
                 acc0 += r[0];
                 if constexpr (PAIR) acc1 += r[N - 1];
-                step_done(i);
-                slab = ns_;
-                b = nbk;
+            };
+            if constexpr (PF) {
+                u32x4 c[N][kQ4Chunks];
 #pragma unroll
-                for (int m = 0; m < N; ++m)
+                for (int m = 0; m < N; ++m) q4_load<LAYOUT>(wm[m], lane, lrow(slab), slab, b, nb, c[m]);
+                for (uint32_t i = i0; i < i1; ++i) {
+                    uint32_t ns_ = slab, nbk = b;
+                    advance(ns_, nbk);
+                    u32x4 nx[N][kQ4Chunks];
+                    if (i + 1 < i1)
 #pragma unroll
-                    for (int k = 0; k < int(kQ4Chunks); ++k) c[m][k] = nx[m][k];
+                        for (int m = 0; m < N; ++m) q4_load<LAYOUT>(wm[m], lane, lrow(ns_), ns_, nbk, nb, nx[m]);
+                    compute(c);
+                    step_done(i);
+                    slab = ns_;
+                    b = nbk;
+#pragma unroll
+                    for (int m = 0; m < N; ++m)
+#pragma unroll
+                        for (int k = 0; k < int(kQ4Chunks); ++k) c[m][k] = nx[m][k];
+                }
+            } else {
+                for (uint32_t i = i0; i < i1; ++i) {
+                    u32x4 c[N][kQ4Chunks];
+#pragma unroll
+                    for (int m = 0; m < N; ++m) q4_load<LAYOUT>(wm[m], lane, lrow(slab), slab, b, nb, c[m]);
+                    compute(c);
+                    step_done(i);
+                    advance(slab, b);
+                }
             }
         } else {
-            u32x4 c0[kQ6Chunks];
-            uint32_t d0 = 0;
-            q6_load<LAYOUT>(w0, lane, lrow(slab), slab, b, nb, c0, d0);
-            for (uint32_t i = i0; i < i1; ++i) {
-                uint32_t ns_ = slab, nbk = b;
-                advance(ns_, nbk);
-                u32x4 n0[kQ6Chunks];
-                uint32_t dn = 0;
-                if (i + 1 < i1) q6_load<LAYOUT>(w0, lane, lrow(ns_), ns_, nbk, nb, n0, dn);
+            auto compute = [&](const u32x4(&cc)[kQ6Chunks], uint32_t dd) {
                 const float *xb = x + size_t(b) * kQK;
                 float xs[16];
                 group_sums<16>(xb, lane, xs);
-                acc0 += q6_dot(c0, d0, xb, xs);
-                step_done(i);
-                slab = ns_;
-                b = nbk;
+                acc0 += q6_dot(cc, dd, xb, xs);
+            };
+            if constexpr (PF) {
+                u32x4 c0[kQ6Chunks];
+                uint32_t d0 = 0;
+                q6_load<LAYOUT>(w0, lane, lrow(slab), slab, b, nb, c0, d0);
+                for (uint32_t i = i0; i < i1; ++i) {
+                    uint32_t ns_ = slab, nbk = b;
+                    advance(ns_, nbk);
+                    u32x4 n0[kQ6Chunks];
+                    uint32_t dn = 0;
+                    if (i + 1 < i1) q6_load<LAYOUT>(w0, lane, lrow(ns_), ns_, nbk, nb, n0, dn);
+                    compute(c0, d0);
+                    step_done(i);
+                    slab = ns_;
+                    b = nbk;
 #pragma unroll
-                for (int k = 0; k < int(kQ6Chunks); ++k) c0[k] = n0[k];
-                d0 = dn;
+                    for (int k = 0; k < int(kQ6Chunks); ++k) c0[k] = n0[k];
+                    d0 = dn;
+                }
+            } else {
+                for (uint32_t i = i0; i < i1; ++i) {
+                    u32x4 c0[kQ6Chunks];
+                    uint32_t d0 = 0;
+                    q6_load<LAYOUT>(w0, lane, lrow(slab), slab, b, nb, c0, d0);
+                    compute(c0, d0);
+                    step_done(i);
+                    advance(slab, b);
+                }
             }
         }
     }
@@ -746,9 +782,9 @@ int env_int(const char *name, int dflt) {
     return v && *v ? atoi(v) : dflt;
 }
 
-template <int TYPE, int LAYOUT, bool PAIR>
+template <int TYPE, int LAYOUT, bool PAIR, bool PF>
 constexpr auto kernel_of() {
-    return &gemv_kernel<TYPE, LAYOUT, PAIR>;
+    return &gemv_kernel<TYPE, LAYOUT, PAIR, PF>;
 }
 
 // Resident waves per CU of one kernel instance, and the CU count, per device.
@@ -768,7 +804,7 @@ DeviceShape device_shape() {
     return d;
 }
 
-template <int TYPE, int LAYOUT, bool PAIR>
+template <int TYPE, int LAYOUT, bool PAIR, bool PF>
 int waves_per_cu() {
     static int cache[64] = {};
     int dev = 0;
@@ -776,7 +812,7 @@ int waves_per_cu() {
     int &w = cache[dev & 63];
     if (w == 0) {
         int wgs = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&wgs, kernel_of<TYPE, LAYOUT, PAIR>(), kWgWaves * 64, 0) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&wgs, kernel_of<TYPE, LAYOUT, PAIR, PF>(), kWgWaves * 64, 0) !=
                 hipSuccess || wgs <= 0)
             wgs = 2;
         w = wgs * kWgWaves;
@@ -814,33 +850,82 @@ GemvPlan plan_gemv(uint32_t cols, uint32_t rows, int resident_waves, uint32_t ma
     return p;
 }
 
-template <int TYPE, bool PAIR>
+template <int TYPE, bool PAIR, bool PF>
 int resident_waves(int layout) {
     const int cus = device_shape().cus;
-    if (layout == CDNA4) return cus * waves_per_cu<TYPE, CDNA4, PAIR>();
-    if (layout == NSMFFN) return cus * waves_per_cu<TYPE, NSMFFN, PAIR>();
-    return cus * waves_per_cu<TYPE, ROW_MAJOR, PAIR>();
+    if (layout == CDNA4) return cus * waves_per_cu<TYPE, CDNA4, PAIR, PF>();
+    if (layout == NSMFFN) return cus * waves_per_cu<TYPE, NSMFFN, PAIR, PF>();
+    return cus * waves_per_cu<TYPE, ROW_MAJOR, PAIR, PF>();
 }
 
-int resident_waves_for(int type, int layout, bool pair) {
-    if (pair) return resident_waves<Q4_K, true>(layout);
-    if (type == Q4_K) return resident_waves<Q4_K, false>(layout);
-    return resident_waves<Q6_K, false>(layout);
+// One unit per wave (the instance without PF): whole slabs per workgroup when a
+// slab has at most 16 super-blocks per row, a CU holds that many waves of the
+// instance (cu_waves) and the slabs fit one workgroup per CU, else the
+// flattened split over 4-wave workgroups.
+GemvPlan plan_one_unit(uint32_t cols, uint32_t rows, uint32_t cus, uint32_t cu_waves) {
+    GemvPlan p;
+    const uint32_t nb = cols / kQK;
+    p.nslabs = (rows + kRowTile - 1) / kRowTile;
+    if (nb <= 16 && nb <= cu_waves && p.nslabs <= cus) {
+        p.W = nb;
+        p.G = p.nslabs;
+    } else {
+        p.W = kWgWaves;
+        p.G = (p.nslabs * nb + kWgWaves - 1) / kWgWaves;
+    }
+    return p;
+}
+
+struct GemvChoice {
+    GemvPlan plan;
+    bool pf;
+};
+
+// The prefetching instance streams many units per wave (the lm-head: 61,440
+// units).  When the device keeps a wave resident for every unit of the
+// instance without the prefetch buffer (the gate/up pair and the down
+// projection: 3,600 units), that instance runs with one unit per wave: every
+// load is issued at launch and each wave computes as soon as its own unit
+// arrives.  NS_GEMV_PF=0/1 forces either instance.
+template <int TYPE, bool PAIR>
+GemvChoice choose_gemv(int layout, uint32_t cols, uint32_t rows) {
+    const uint32_t cus = uint32_t(device_shape().cus);
+    const uint32_t nb = cols / kQK, units = ((rows + kRowTile - 1) / kRowTile) * nb;
+    const int force = env_int("NS_GEMV_PF", -1);
+    const bool one = force == 0 || (force < 0 && int(units) <= resident_waves<TYPE, PAIR, false>(layout));
+    if (one) return {plan_one_unit(cols, rows, cus, uint32_t(resident_waves<TYPE, PAIR, false>(layout)) / cus), false};
+    return {plan_gemv(cols, rows, resident_waves<TYPE, PAIR, true>(layout), max_wg_waves(TYPE, PAIR, true), cus),
+            true};
+}
+
+GemvChoice choose_gemv_for(int type, int layout, bool pair, uint32_t cols, uint32_t rows) {
+    if (pair) return choose_gemv<Q4_K, true>(layout, cols, rows);
+    if (type == Q4_K) return choose_gemv<Q4_K, false>(layout, cols, rows);
+    return choose_gemv<Q6_K, false>(layout, cols, rows);
+}
+
+template <int TYPE, bool PAIR, bool PF>
+void launch_instance(int layout, const GemvPlan &p, const uint8_t *w, const uint8_t *up, const float *x, float *out,
+                     uint32_t cols, uint32_t rows, const Workspace &ws, hipStream_t stream) {
+    const uint32_t nb = cols / kQK;
+    const dim3 grid(p.G), block(p.W * 64);
+    if (layout == CDNA4)
+        gemv_kernel<TYPE, CDNA4, PAIR, PF><<<grid, block, 0, stream>>>(w, up, x, out, rows, nb, p.nslabs, ws.partial,
+                                                                      ws.counters);
+    else if (layout == NSMFFN)
+        gemv_kernel<TYPE, NSMFFN, PAIR, PF><<<grid, block, 0, stream>>>(w, up, x, out, rows, nb, p.nslabs, ws.partial,
+                                                                       ws.counters);
+    else
+        gemv_kernel<TYPE, ROW_MAJOR, PAIR, PF><<<grid, block, 0, stream>>>(w, up, x, out, rows, nb, p.nslabs,
+                                                                          ws.partial, ws.counters);
 }
 
 template <int TYPE, bool PAIR>
 hipError_t launch_typed(int layout, const uint8_t *w, const uint8_t *up, const float *x, float *out,
                         uint32_t cols, uint32_t rows, const Workspace &ws, hipStream_t stream) {
-    const GemvPlan p = plan_gemv(cols, rows, resident_waves<TYPE, PAIR>(layout), max_wg_waves(TYPE, PAIR),
-                                 uint32_t(device_shape().cus));
-    const uint32_t nb = cols / kQK;
-    const dim3 grid(p.G), block(p.W * 64);
-    if (layout == CDNA4)
-        gemv_kernel<TYPE, CDNA4, PAIR><<<grid, block, 0, stream>>>(w, up, x, out, rows, nb, p.nslabs, ws.partial, ws.counters);
-    else if (layout == NSMFFN)
-        gemv_kernel<TYPE, NSMFFN, PAIR><<<grid, block, 0, stream>>>(w, up, x, out, rows, nb, p.nslabs, ws.partial, ws.counters);
-    else
-        gemv_kernel<TYPE, ROW_MAJOR, PAIR><<<grid, block, 0, stream>>>(w, up, x, out, rows, nb, p.nslabs, ws.partial, ws.counters);
+    const GemvChoice c = choose_gemv<TYPE, PAIR>(layout, cols, rows);
+    if (c.pf) launch_instance<TYPE, PAIR, true>(layout, c.plan, w, up, x, out, cols, rows, ws, stream);
+    else launch_instance<TYPE, PAIR, false>(layout, c.plan, w, up, x, out, cols, rows, ws, stream);
     return hipGetLastError();
 }
 
@@ -894,8 +979,7 @@ uint32_t mt_tokens(uint32_t batch, bool xh) { return xh && batch <= 2 ? 2u : 4u;
 
 void gemv_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, bool pair, size_t *partial_floats,
                          size_t *counters) {
-    const GemvPlan p = plan_gemv(cols, rows, resident_waves_for(type, layout, pair),
-                                 max_wg_waves(pair ? Q4_K : type, pair), uint32_t(device_shape().cus));
+    const GemvPlan p = choose_gemv_for(type, layout, pair, cols, rows).plan;
     *partial_floats = size_t(p.G) * 2 * 64 * (pair ? 2 : 1);
     *counters = p.nslabs;
 }
