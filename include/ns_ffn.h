@@ -113,15 +113,31 @@ int ns_ffn_down(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols,
 int ns_dequant(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, uint32_t rows,
                uint32_t row0, uint32_t nrows, float *out_f32, uint16_t *out_f16, void *stream);
 
-/* Inter-layer step of BASELINE config 4 (the 48-layer FFN stack), which keeps the hidden
- * state an N(0,1) vector at unit RMS: per token, out[t] = (y[t] - m) / sqrt(mean_k (y[t][k] - m)^2)
- * with m = mean_k y[t][k], as fp16 bits (out_half != 0) or fp32; a constant row maps to zeros.
- * The mean is removed because the synthetic weights have a positive mean that makes an uncentred
- * chain collapse.  It takes the place of the engine's residual-add + RMSNorm between FFN blocks
- * (rms_add_then_half, metal:523-529; mm:563, mm:574), which is outside this path.
- * y fp32 [batch][cols]. */
-int ns_standardize(ns_ctx *ctx, const float *y, uint32_t batch, uint32_t cols, void *out, int out_half,
-                   void *stream);
+/* The engine's RMSNorm family around the FFN block (metal:509-529; rms, rms_half, rms_add,
+ * rms_add_then_half at mm:291-296, called at mm:563, mm:574, mm:576).  Per row of `width`
+ * (`rows` rows), r = 1/sqrt(mean(x^2) + eps):
+ *   ns_rmsnorm:          y = (x*r)*weight, fp32 or fp16 bits (half_out): rms / rms_half.
+ *   ns_rmsnorm_add:      y = residual + (x*r)*weight, times *scale when scale is non-NULL:
+ *                        rms_add (gemma_rmsnorm_add[_scale]).
+ *   ns_rmsnorm_add_then: y as ns_rmsnorm_add, then next = (y*r2)*next_weight with r2 taken
+ *                        over y, as fp16 bits (half_next: rms_add_then_half) or fp32 (rms_add
+ *                        followed by rms, the decode order at mm:563).
+ * Device pointers; scale points at one fp32 (a layer's out_scale tensor).  y may alias x or
+ * residual (each element is read before it is written, by the same thread). */
+int ns_rmsnorm(ns_ctx *ctx, const float *x, const float *weight, uint32_t rows, uint32_t width, float eps,
+               void *y, int half_out, void *stream);
+int ns_rmsnorm_add(ns_ctx *ctx, const float *x, const float *weight, const float *residual, const float *scale,
+                   uint32_t rows, uint32_t width, float eps, float *y, void *stream);
+int ns_rmsnorm_add_then(ns_ctx *ctx, const float *x, const float *weight, const float *residual,
+                        const float *scale, const float *next_weight, uint32_t rows, uint32_t width, float eps,
+                        float *y, void *next, int half_next, void *stream);
+
+/* rms (mm:563, the decode branch) fused into gate_up_geglu_decode (mm:571), one launch:
+ * h[r] = gelu_tanh(Wg[r].n) * (Wu[r].n) with n = (x*r)*norm_weight, r = 1/sqrt(mean(x^2) + eps).
+ * Q4_K gate/up; cols <= 16384; x and norm_weight 16-byte aligned; fp32 x, h. */
+int ns_rms_gate_up_geglu_decode(ns_ctx *ctx, const void *wg, const void *wu, int layout, uint32_t cols,
+                                uint32_t rows, const float *x, const float *norm_weight, float eps, float *h,
+                                void *stream);
 
 /* ---- host-side (CPU) utilities; no GPU needed ------------------------------ */
 

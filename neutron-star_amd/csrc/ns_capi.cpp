@@ -221,10 +221,61 @@ extern "C" int ns_retile_device(const void *src, void *dst, int type, uint32_t c
     return e == hipSuccess ? NS_OK : hip_fail(e, "ns_retile_device");
 }
 
-extern "C" int ns_standardize(ns_ctx *ctx, const float *y, uint32_t batch, uint32_t cols, void *out, int out_half,
-                              void *stream) {
-    if (!ctx) return fail(NS_ERR_ARG, "ns_standardize: null context");
-    if (!y || !out || batch == 0 || cols == 0) return fail(NS_ERR_ARG, "ns_standardize: null buffer or empty shape");
-    const hipError_t e = launch_standardize(y, batch, cols, out, out_half != 0, static_cast<hipStream_t>(stream));
-    return e == hipSuccess ? NS_OK : hip_fail(e, "ns_standardize");
+extern "C" int ns_rmsnorm(ns_ctx *ctx, const float *x, const float *weight, uint32_t rows, uint32_t width, float eps,
+                          void *y, int half_out, void *stream) {
+    if (!ctx) return fail(NS_ERR_ARG, "ns_rmsnorm: null context");
+    if (!x || !weight || !y || rows == 0 || width == 0) return fail(NS_ERR_ARG, "ns_rmsnorm: null buffer or empty shape");
+    const hipError_t e = launch_rmsnorm(x, weight, nullptr, nullptr, nullptr, rows, width, eps, y, half_out != 0,
+                                        nullptr, false, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? NS_OK : hip_fail(e, "ns_rmsnorm");
+}
+
+extern "C" int ns_rmsnorm_add(ns_ctx *ctx, const float *x, const float *weight, const float *residual,
+                              const float *scale, uint32_t rows, uint32_t width, float eps, float *y, void *stream) {
+    if (!ctx) return fail(NS_ERR_ARG, "ns_rmsnorm_add: null context");
+    if (!x || !weight || !residual || !y || rows == 0 || width == 0)
+        return fail(NS_ERR_ARG, "ns_rmsnorm_add: null buffer or empty shape");
+    const hipError_t e = launch_rmsnorm(x, weight, residual, scale, nullptr, rows, width, eps, y, false, nullptr,
+                                        false, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? NS_OK : hip_fail(e, "ns_rmsnorm_add");
+}
+
+extern "C" int ns_rmsnorm_add_then(ns_ctx *ctx, const float *x, const float *weight, const float *residual,
+                                   const float *scale, const float *next_weight, uint32_t rows, uint32_t width,
+                                   float eps, float *y, void *next, int half_next, void *stream) {
+    if (!ctx) return fail(NS_ERR_ARG, "ns_rmsnorm_add_then: null context");
+    if (!x || !weight || !residual || !next_weight || !y || !next || rows == 0 || width == 0)
+        return fail(NS_ERR_ARG, "ns_rmsnorm_add_then: null buffer or empty shape");
+    const hipError_t e = launch_rmsnorm(x, weight, residual, scale, next_weight, rows, width, eps, y, false, next,
+                                        half_next != 0, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? NS_OK : hip_fail(e, "ns_rmsnorm_add_then");
+}
+
+namespace {
+int rms_gate_up(ns_ctx *ctx, const char *fn, const void *wg, const void *wu, int layout, uint32_t cols,
+                uint32_t rows, const NormPrologue &np, float *h, void *stream) {
+    if (!ctx) return fail(NS_ERR_ARG, std::string(fn) + ": null context");
+    if (int rc = check_tensor(fn, wg, Q4_K, layout, cols, rows)) return rc;
+    if (int rc = check_tensor(fn, wu, Q4_K, layout, cols, rows)) return rc;
+    if (!np.x || !np.wb || !h) return fail(NS_ERR_ARG, std::string(fn) + ": null input/output");
+    if (cols > 16384) return fail(NS_ERR_SHAPE, std::string(fn) + ": cols above 16384 (the LDS copy of x)");
+    if ((reinterpret_cast<uintptr_t>(np.x) | reinterpret_cast<uintptr_t>(np.wb)) % 16)
+        return fail(NS_ERR_ARG, std::string(fn) + ": x and norm_weight must be 16-byte aligned");
+    size_t pf = 0, nc = 0;
+    gemv_workspace_need(Q4_K, layout, cols, rows, true, &pf, &nc);
+    if (int rc = ensure_ws(ctx, pf, nc)) return rc;
+    const hipError_t e = launch_gemv(Q4_K, layout, static_cast<const uint8_t *>(wg), static_cast<const uint8_t *>(wu),
+                                     nullptr, h, cols, rows, ctx->ws, static_cast<hipStream_t>(stream), &np);
+    return e == hipSuccess ? NS_OK : hip_fail(e, fn);
+}
+}  // namespace
+
+extern "C" int ns_rms_gate_up_geglu_decode(ns_ctx *ctx, const void *wg, const void *wu, int layout, uint32_t cols,
+                                           uint32_t rows, const float *x, const float *norm_weight, float eps,
+                                           float *h, void *stream) {
+    NormPrologue np;
+    np.x = x;
+    np.wb = norm_weight;
+    np.eps = eps;
+    return rms_gate_up(ctx, "ns_rms_gate_up_geglu_decode", wg, wu, layout, cols, rows, np, h, stream);
 }

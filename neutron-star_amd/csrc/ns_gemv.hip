@@ -27,6 +27,7 @@
 // exactly; the 2^24 / 2^20 factors are folded into the group scale.
 #include "ns_internal.hpp"
 #include "ns_quant.hpp"
+#include "ns_rms.hpp"
 
 namespace ns {
 namespace {
@@ -369,28 +370,96 @@ struct Split {
     }
 };
 
+// NormPrologue (ns_internal.hpp) into xn[0..cols) by the whole workgroup (the
+// XL 1 form).  Rows of at most one float4 per thread (the 3,840-wide input over
+// the 15 waves of a whole-slab workgroup) are held in registers: norm_load issues
+// their loads before the kernel requests its first weights, and norm_finish then
+// waits for those loads only.  Longer rows take a looped form in norm_finish.
+// Every workgroup computes the same values in the same order.
+__device__ __forceinline__ bool norm_in_regs(uint32_t cols) { return cols / 4 <= blockDim.x; }
+
+__device__ __forceinline__ void norm_load(RmsRow<1> &rr, const NormPrologue &np, uint32_t cols) {
+    if (norm_in_regs(cols))
+        rms_row_load<1>(rr, reinterpret_cast<const float4 *>(np.x), reinterpret_cast<const float4 *>(np.wb), nullptr,
+                        nullptr, nullptr, cols / 4);
+}
+
+__device__ void norm_finish(RmsRow<1> &rr, const NormPrologue &np, uint32_t cols, float *xn, float *part,
+                            uint32_t nw) {
+    const uint32_t nt = blockDim.x, tid = threadIdx.x;
+    if (norm_in_regs(cols)) {
+        float4 *xn4 = reinterpret_cast<float4 *>(xn);
+        rms_row_finish<1>(rr, false, false, false, cols / 4, np.eps, part,
+                          [&](uint32_t j, const float4 &v) { xn4[j] = v; }, [](uint32_t, const float4 &) {});
+    } else {
+        float s = 0.f;
+        for (uint32_t k = tid; k < cols; k += nt) s = __builtin_fmaf(np.x[k], np.x[k], s);
+        const float r = rms_factor(wg_sum(s, part, nw), cols, np.eps);
+        for (uint32_t k = tid; k < cols; k += nt) xn[k] = (np.x[k] * r) * np.wb[k];
+    }
+    __syncthreads();
+}
+
 // PF: the next unit's weights are loaded while one is computed (the streaming
 // regime, many units per wave).  Without PF a wave loads and computes one unit
 // at a time; that instance needs fewer registers, so a CU holds twice the waves
 // of the gate/up pair, and a grid with one unit per wave issues every load at
 // launch.
-template <int TYPE, int LAYOUT, bool PAIR, bool PF>
+// XL (the NormPrologue forms; dynamic LDS of cols floats; the dot products
+// read x from LDS):
+//   1: every workgroup first builds the whole normalised vector (ns::rms_row or
+//      a loop); the weights of each wave's first unit are requested before the
+//      prologue's arithmetic, so its reads overlap their latency;
+//   2: on a whole-slab grid of one super-block per wave (W = nb):
+//      the waves of a workgroup together cover x exactly once, so each wave
+//      forms only its own block x*w in LDS and its own sum of squares, with no
+//      barrier; r = 1/sqrt(mean(x^2) + eps) multiplies the finished dot
+//      products in the final combine (W.((x*r)*w) = r * W.(x*w) to rounding).
+//      A workgroup barrier at the start would hold every wave until the last
+//      one of its workgroup had been dispatched and had its row.
+template <int TYPE, int LAYOUT, bool PAIR, bool PF, int XL>
 __global__ __launch_bounds__(max_wg_waves(TYPE, PAIR, PF) * 64) void gemv_kernel(
-    const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, const float *__restrict__ x,
+    const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, const float *__restrict__ xg,
     float *__restrict__ out, uint32_t rows, uint32_t nb, uint32_t nslabs, float *__restrict__ partial,
-    uint32_t *__restrict__ counters) {
+    uint32_t *__restrict__ counters, const NormPrologue np) {
     constexpr uint32_t kPlanes = PAIR ? 2 : 1;
     constexpr uint32_t kMaxW = max_wg_waves(TYPE, PAIR, PF);
     __shared__ float lds_part[kMaxW][2][kPlanes][64];
     __shared__ uint32_t lds_slab[kMaxW][2];
+    __shared__ float lds_sum[kMaxW];
+    extern __shared__ __attribute__((aligned(16))) float lds_x[];
     const uint32_t nw = blockDim.x >> 6;  // waves in this workgroup (<= kMaxW)
-
+    const float *__restrict__ x = XL ? lds_x : xg;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t G = gridDim.x, g = blockIdx.x, U = nslabs * nb;
     const Split sp{U / G, U % G};
     const uint32_t wg0 = sp.first(g), wg1 = sp.first(g + 1), n = wg1 - wg0;
     const uint32_t i0 = wg0 + wave * n / nw, i1 = wg0 + (wave + 1) * n / nw;
+
+    RmsRow<1> rr;
+    float4 xv{}, wv{};
+    float xsq = 0.f;  // XL 2: this wave's sum of squares of its block of x
+    if constexpr (XL == 1) norm_load(rr, np, nb * kQK);
+    if constexpr (XL == 2) {
+        const uint32_t blk = i0 % nb;
+        xv = reinterpret_cast<const float4 *>(np.x)[blk * (kQK / 4) + lane];
+        wv = reinterpret_cast<const float4 *>(np.wb)[blk * (kQK / 4) + lane];
+    }
+    auto prologue = [&]() {
+        if constexpr (XL == 1) norm_finish(rr, np, nb * kQK, lds_x, lds_sum, nw);
+        if constexpr (XL == 2) {
+            const uint32_t blk = i0 % nb;
+            reinterpret_cast<float4 *>(lds_x)[blk * (kQK / 4) + lane] =
+                float4{xv.x * wv.x, xv.y * wv.y, xv.z * wv.z, xv.w * wv.w};
+            float sq = sumsq4(xv, 0.f);
+            for (int m = 32; m >= 1; m >>= 1) sq += __shfl_xor(sq, m);
+            xsq = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sq)));
+            if (lane == 0) lds_sum[wave] = xsq;
+        }
+    };
+    // XL 2: the factor r applied to finished sums (ts: the sum of squares of all of x)
+    auto rms_scale = [&](float ts) { return rms_factor(ts, nb * kQK, np.eps); };
 
     if (lane < 2) lds_slab[wave][lane] = ~0u;
     float acc0 = 0.f, acc1 = 0.f;
@@ -401,6 +470,11 @@ __global__ __launch_bounds__(max_wg_waves(TYPE, PAIR, PF) * 64) void gemv_kernel
         if (b == nb - 1 || i + 1 == i1) {
             if (seg_b0 == 0 && b == nb - 1) {
                 const uint32_t row = slab * kRowTile + lane;
+                if (XL == 2) {  // one wave covers the whole row (nb == 1)
+                    const float r = rms_scale(xsq);
+                    acc0 *= r;
+                    acc1 *= r;
+                }
                 if (row < rows) {
                     if constexpr (PAIR) out[row] = gelu_tanh(acc0) * acc1;
                     else out[row] = acc0;
@@ -425,82 +499,94 @@ __global__ __launch_bounds__(max_wg_waves(TYPE, PAIR, PF) * 64) void gemv_kernel
         }
     };
 
-    if (i0 < i1) {
-        if constexpr (TYPE == Q4_K) {
-            constexpr int N = PAIR ? 2 : 1;
-            const uint8_t *wm[2] = {w0, w1};
-            auto compute = [&](const u32x4(&cc)[N][kQ4Chunks]) {
-                const float *xb = x + size_t(b) * kQK;
-                float xs[8], r[N];
-                group_sums<32>(xb, lane, xs);
-                q4_dot<N>(cc, xb, xs, r);
-                acc0 += r[0];
-                if constexpr (PAIR) acc1 += r[N - 1];
-            };
-            if constexpr (PF) {
-                u32x4 c[N][kQ4Chunks];
+    // Each branch requests the first unit's weights, runs the prologue (all
+    // threads of the workgroup: it has barriers), then walks the wave's units.
+    if constexpr (TYPE == Q4_K) {
+        constexpr int N = PAIR ? 2 : 1;
+        const uint8_t *wm[2] = {w0, w1};
+        auto compute = [&](const u32x4(&cc)[N][kQ4Chunks]) {
+            const float *xb = x + size_t(b) * kQK;
+            float xs[8], r[N];
+            group_sums<32>(xb, lane, xs);
+            q4_dot<N>(cc, xb, xs, r);
+            acc0 += r[0];
+            if constexpr (PAIR) acc1 += r[N - 1];
+        };
+        u32x4 c[N][kQ4Chunks];
+        if constexpr (XL) {
+            // Unconditional (a wave without units loads the last unit and drops it), so
+            // the wait for the prologue's row counts these loads as still outstanding.
+            const uint32_t iu = i0 < U ? i0 : U - 1, su = iu / nb, bu = iu - su * nb;
+#pragma unroll
+            for (int m = 0; m < N; ++m) q4_load<LAYOUT>(wm[m], lane, lrow(su), su, bu, nb, c[m]);
+        } else if constexpr (PF) {
+            if (i0 < i1)
 #pragma unroll
                 for (int m = 0; m < N; ++m) q4_load<LAYOUT>(wm[m], lane, lrow(slab), slab, b, nb, c[m]);
-                for (uint32_t i = i0; i < i1; ++i) {
-                    uint32_t ns_ = slab, nbk = b;
-                    advance(ns_, nbk);
-                    u32x4 nx[N][kQ4Chunks];
-                    if (i + 1 < i1)
+        }
+        prologue();
+        if constexpr (PF) {
+            for (uint32_t i = i0; i < i1; ++i) {
+                uint32_t ns_ = slab, nbk = b;
+                advance(ns_, nbk);
+                u32x4 nx[N][kQ4Chunks];
+                if (i + 1 < i1)
 #pragma unroll
-                        for (int m = 0; m < N; ++m) q4_load<LAYOUT>(wm[m], lane, lrow(ns_), ns_, nbk, nb, nx[m]);
-                    compute(c);
-                    step_done(i);
-                    slab = ns_;
-                    b = nbk;
+                    for (int m = 0; m < N; ++m) q4_load<LAYOUT>(wm[m], lane, lrow(ns_), ns_, nbk, nb, nx[m]);
+                compute(c);
+                step_done(i);
+                slab = ns_;
+                b = nbk;
 #pragma unroll
-                    for (int m = 0; m < N; ++m)
+                for (int m = 0; m < N; ++m)
 #pragma unroll
-                        for (int k = 0; k < int(kQ4Chunks); ++k) c[m][k] = nx[m][k];
-                }
-            } else {
-                for (uint32_t i = i0; i < i1; ++i) {
-                    u32x4 c[N][kQ4Chunks];
+                    for (int k = 0; k < int(kQ4Chunks); ++k) c[m][k] = nx[m][k];
+            }
+        } else if constexpr (XL == 2) {
+            compute(c);  // exactly one unit per wave (W = nb, one slab per workgroup)
+            step_done(i0);
+        } else {
+            for (uint32_t i = i0; i < i1; ++i) {
+                if (!XL || i != i0)
 #pragma unroll
                     for (int m = 0; m < N; ++m) q4_load<LAYOUT>(wm[m], lane, lrow(slab), slab, b, nb, c[m]);
-                    compute(c);
-                    step_done(i);
-                    advance(slab, b);
-                }
+                compute(c);
+                step_done(i);
+                advance(slab, b);
+            }
+        }
+    } else {
+        auto compute = [&](const u32x4(&cc)[kQ6Chunks], uint32_t dd) {
+            const float *xb = x + size_t(b) * kQK;
+            float xs[16];
+            group_sums<16>(xb, lane, xs);
+            acc0 += q6_dot(cc, dd, xb, xs);
+        };
+        u32x4 c0[kQ6Chunks];
+        uint32_t d0 = 0;
+        if ((PF || XL) && i0 < i1) q6_load<LAYOUT>(w0, lane, lrow(slab), slab, b, nb, c0, d0);
+        prologue();
+        if constexpr (PF) {
+            for (uint32_t i = i0; i < i1; ++i) {
+                uint32_t ns_ = slab, nbk = b;
+                advance(ns_, nbk);
+                u32x4 n0[kQ6Chunks];
+                uint32_t dn = 0;
+                if (i + 1 < i1) q6_load<LAYOUT>(w0, lane, lrow(ns_), ns_, nbk, nb, n0, dn);
+                compute(c0, d0);
+                step_done(i);
+                slab = ns_;
+                b = nbk;
+#pragma unroll
+                for (int k = 0; k < int(kQ6Chunks); ++k) c0[k] = n0[k];
+                d0 = dn;
             }
         } else {
-            auto compute = [&](const u32x4(&cc)[kQ6Chunks], uint32_t dd) {
-                const float *xb = x + size_t(b) * kQK;
-                float xs[16];
-                group_sums<16>(xb, lane, xs);
-                acc0 += q6_dot(cc, dd, xb, xs);
-            };
-            if constexpr (PF) {
-                u32x4 c0[kQ6Chunks];
-                uint32_t d0 = 0;
-                q6_load<LAYOUT>(w0, lane, lrow(slab), slab, b, nb, c0, d0);
-                for (uint32_t i = i0; i < i1; ++i) {
-                    uint32_t ns_ = slab, nbk = b;
-                    advance(ns_, nbk);
-                    u32x4 n0[kQ6Chunks];
-                    uint32_t dn = 0;
-                    if (i + 1 < i1) q6_load<LAYOUT>(w0, lane, lrow(ns_), ns_, nbk, nb, n0, dn);
-                    compute(c0, d0);
-                    step_done(i);
-                    slab = ns_;
-                    b = nbk;
-#pragma unroll
-                    for (int k = 0; k < int(kQ6Chunks); ++k) c0[k] = n0[k];
-                    d0 = dn;
-                }
-            } else {
-                for (uint32_t i = i0; i < i1; ++i) {
-                    u32x4 c0[kQ6Chunks];
-                    uint32_t d0 = 0;
-                    q6_load<LAYOUT>(w0, lane, lrow(slab), slab, b, nb, c0, d0);
-                    compute(c0, d0);
-                    step_done(i);
-                    advance(slab, b);
-                }
+            for (uint32_t i = i0; i < i1; ++i) {
+                if (!XL || i != i0) q6_load<LAYOUT>(w0, lane, lrow(slab), slab, b, nb, c0, d0);
+                compute(c0, d0);
+                step_done(i);
+                advance(slab, b);
             }
         }
     }
@@ -562,6 +648,13 @@ __global__ __launch_bounds__(max_wg_waves(TYPE, PAIR, PF) * 64) void gemv_kernel
                     }
             }
             if (lane == 0) __hip_atomic_store(&counters[s], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if constexpr (XL == 2) {  // whole-slab grid: the workgroup's waves cover all of x
+            float ts = 0.f;
+            for (uint32_t v = 0; v < nw; ++v) ts += lds_sum[v];
+            const float r = rms_scale(ts);
+            r0 *= r;
+            r1 *= r;
         }
         if (row < rows) {
             if constexpr (PAIR) out[row] = gelu_tanh(r0) * r1;
@@ -784,7 +877,7 @@ int env_int(const char *name, int dflt) {
 
 template <int TYPE, int LAYOUT, bool PAIR, bool PF>
 constexpr auto kernel_of() {
-    return &gemv_kernel<TYPE, LAYOUT, PAIR, PF>;
+    return &gemv_kernel<TYPE, LAYOUT, PAIR, PF, 0>;
 }
 
 // Resident waves per CU of one kernel instance, and the CU count, per device.
@@ -904,28 +997,46 @@ GemvChoice choose_gemv_for(int type, int layout, bool pair, uint32_t cols, uint3
     return choose_gemv<Q6_K, false>(layout, cols, rows);
 }
 
-template <int TYPE, bool PAIR, bool PF>
-void launch_instance(int layout, const GemvPlan &p, const uint8_t *w, const uint8_t *up, const float *x, float *out,
-                     uint32_t cols, uint32_t rows, const Workspace &ws, hipStream_t stream) {
+template <int TYPE, int LAYOUT, bool PAIR, bool PF>
+void launch_layout(const GemvPlan &p, const uint8_t *w, const uint8_t *up, const float *x, float *out, uint32_t cols,
+                   uint32_t rows, const Workspace &ws, hipStream_t stream, const NormPrologue *np) {
     const uint32_t nb = cols / kQK;
     const dim3 grid(p.G), block(p.W * 64);
-    if (layout == CDNA4)
-        gemv_kernel<TYPE, CDNA4, PAIR, PF><<<grid, block, 0, stream>>>(w, up, x, out, rows, nb, p.nslabs, ws.partial,
-                                                                      ws.counters);
-    else if (layout == NSMFFN)
-        gemv_kernel<TYPE, NSMFFN, PAIR, PF><<<grid, block, 0, stream>>>(w, up, x, out, rows, nb, p.nslabs, ws.partial,
-                                                                       ws.counters);
-    else
-        gemv_kernel<TYPE, ROW_MAJOR, PAIR, PF><<<grid, block, 0, stream>>>(w, up, x, out, rows, nb, p.nslabs,
-                                                                          ws.partial, ws.counters);
+    if constexpr (PAIR) {
+        if (np) {
+            const size_t lds = size_t(cols) * sizeof(float);
+            if constexpr (!PF) {
+                // the barrier-free form: one super-block per wave, whole slabs
+                if (p.W == nb && p.G == p.nslabs) {
+                    gemv_kernel<TYPE, LAYOUT, PAIR, PF, 2><<<grid, block, lds, stream>>>(
+                        w, up, x, out, rows, nb, p.nslabs, ws.partial, ws.counters, *np);
+                    return;
+                }
+            }
+            gemv_kernel<TYPE, LAYOUT, PAIR, PF, 1><<<grid, block, lds, stream>>>(w, up, x, out, rows, nb, p.nslabs,
+                                                                                ws.partial, ws.counters, *np);
+            return;
+        }
+    }
+    gemv_kernel<TYPE, LAYOUT, PAIR, PF, 0><<<grid, block, 0, stream>>>(w, up, x, out, rows, nb, p.nslabs,
+                                                                      ws.partial, ws.counters, NormPrologue{});
+}
+
+template <int TYPE, bool PAIR, bool PF>
+void launch_instance(int layout, const GemvPlan &p, const uint8_t *w, const uint8_t *up, const float *x, float *out,
+                     uint32_t cols, uint32_t rows, const Workspace &ws, hipStream_t stream, const NormPrologue *np) {
+    if (layout == CDNA4) launch_layout<TYPE, CDNA4, PAIR, PF>(p, w, up, x, out, cols, rows, ws, stream, np);
+    else if (layout == NSMFFN) launch_layout<TYPE, NSMFFN, PAIR, PF>(p, w, up, x, out, cols, rows, ws, stream, np);
+    else launch_layout<TYPE, ROW_MAJOR, PAIR, PF>(p, w, up, x, out, cols, rows, ws, stream, np);
 }
 
 template <int TYPE, bool PAIR>
 hipError_t launch_typed(int layout, const uint8_t *w, const uint8_t *up, const float *x, float *out,
-                        uint32_t cols, uint32_t rows, const Workspace &ws, hipStream_t stream) {
+                        uint32_t cols, uint32_t rows, const Workspace &ws, hipStream_t stream,
+                        const NormPrologue *np) {
     const GemvChoice c = choose_gemv<TYPE, PAIR>(layout, cols, rows);
-    if (c.pf) launch_instance<TYPE, PAIR, true>(layout, c.plan, w, up, x, out, cols, rows, ws, stream);
-    else launch_instance<TYPE, PAIR, false>(layout, c.plan, w, up, x, out, cols, rows, ws, stream);
+    if (c.pf) launch_instance<TYPE, PAIR, true>(layout, c.plan, w, up, x, out, cols, rows, ws, stream, np);
+    else launch_instance<TYPE, PAIR, false>(layout, c.plan, w, up, x, out, cols, rows, ws, stream, np);
     return hipGetLastError();
 }
 
@@ -985,10 +1096,12 @@ void gemv_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, boo
 }
 
 hipError_t launch_gemv(int type, int layout, const uint8_t *w, const uint8_t *up, const float *x,
-                       float *out, uint32_t cols, uint32_t rows, const Workspace &ws, hipStream_t stream) {
-    if (up) return launch_typed<Q4_K, true>(layout, w, up, x, out, cols, rows, ws, stream);
-    if (type == Q4_K) return launch_typed<Q4_K, false>(layout, w, nullptr, x, out, cols, rows, ws, stream);
-    return launch_typed<Q6_K, false>(layout, w, nullptr, x, out, cols, rows, ws, stream);
+                       float *out, uint32_t cols, uint32_t rows, const Workspace &ws, hipStream_t stream,
+                       const NormPrologue *np) {
+    if (up) return launch_typed<Q4_K, true>(layout, w, up, x, out, cols, rows, ws, stream, np);
+    if (np) return hipErrorInvalidValue;  // the prologue exists for the gate/up pair only
+    if (type == Q4_K) return launch_typed<Q4_K, false>(layout, w, nullptr, x, out, cols, rows, ws, stream, nullptr);
+    return launch_typed<Q6_K, false>(layout, w, nullptr, x, out, cols, rows, ws, stream, nullptr);
 }
 
 void gemv_mt_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, bool pair, uint32_t batch, bool xh,

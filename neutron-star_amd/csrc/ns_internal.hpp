@@ -22,11 +22,21 @@ struct Workspace {
     size_t counter_count = 0;
 };
 
+// The RMSNorm ahead of the FFN (rms: metal:510-511, mm:563), applied by a
+// decode GEMV to its input: the dot products take xn = (x * r) * wb with
+// r = 1/sqrt(mean(x^2) + eps).
+struct NormPrologue {
+    const float *x = nullptr, *wb = nullptr;
+    float eps = 0.f;
+};
+
 // Decode GEMV: out[r] = sum_k W[r,k] x[k] (fp32).  With `up` non-null, the
-// gate/up pair with the GeGLU epilogue (out = h).  Returns a hipError_t.
+// gate/up pair with the GeGLU epilogue (out = h).  With `np` non-null (the
+// gate/up pair only), x is ignored and the dot products take np's normalised
+// vector.  Returns a hipError_t.
 hipError_t launch_gemv(int type, int layout, const uint8_t *w, const uint8_t *up,
                        const float *x, float *out, uint32_t cols, uint32_t rows,
-                       const Workspace &ws, hipStream_t stream);
+                       const Workspace &ws, hipStream_t stream, const NormPrologue *np = nullptr);
 
 // Required workspace for launch_gemv with these shapes.
 void gemv_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, bool pair, size_t *partial_floats,
@@ -64,8 +74,15 @@ hipError_t launch_dequant(int type, int layout, const uint8_t *w, uint32_t cols,
                           uint32_t row0, uint32_t nrows, float *out_f32, uint16_t *out_f16,
                           hipStream_t stream);
 
-// x[t] = (y[t] - mean(y[t])) / rms(y[t] - mean(y[t])) per token, fp16 (half) or fp32 out.
-hipError_t launch_standardize(const float *y, uint32_t batch, uint32_t cols, void *out, bool half, hipStream_t stream);
+// Row-wise RMSNorm family (metal:509-529), one workgroup per row of `width`:
+//   y = (x * r) * w                                 (residual == nullptr)
+//   y = (residual + (x * r) * w) [* *scale]         (residual != nullptr; fp32 y)
+// r = rsqrt(mean(x^2) + eps).  With next_w non-null, also next = (y * r2) * next_w,
+// r2 = rsqrt(mean(y^2) + eps) (rms_add_then_f16 and its fp32 form).  half_y / half_next
+// select fp16 outputs.
+hipError_t launch_rmsnorm(const float *x, const float *w, const float *residual, const float *scale,
+                          const float *next_w, uint32_t rows, uint32_t width, float eps, void *y, bool half_y,
+                          void *next, bool half_next, hipStream_t stream);
 
 hipError_t launch_retile(int type, const uint8_t *src, uint8_t *dst, uint32_t cols,
                          uint32_t rows, int from_layout, int to_layout, hipStream_t stream);

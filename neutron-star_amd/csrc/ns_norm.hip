@@ -1,25 +1,11 @@
-// ns_norm.hip -- standardisation of FFN outputs between layers of the stack.
-//
-// BASELINE config 4 keeps the hidden state of the 48-layer FFN stack an N(0,1)
-// vector at unit RMS between layers: x_t = (y_t - mean(y_t)) / rms(y_t - mean(y_t))
-// per token, as fp16 for the prefill GEMMs (the engine's halfbuf,
-// metal_engine.mm:563) or fp32 for the decode GEMVs (its `norm` buffer).  It
-// stands in for the engine's residual-add + RMSNorm between FFN blocks
-// (rms_add_then_half, metal:523-529), which is outside this path.
-//
-// The mean is removed because BASELINE's synthetic weights are not centred:
-// a Q4_K weight d*sc*q - dmin*m with d, dmin = |N|*1e-3 and uniform sc, m, q
-// has mean ~0.16, so every output of a layer carries a common component
-// proportional to sum(x).  A chain that only rescales drifts towards a constant
-// vector within a few layers; once that constant is negative every gate output
-// is far below zero, GeGLU returns exactly 0, and the next rescale is 0/0.
-// A row whose values are all equal maps to zeros.
-//
-// One workgroup per token; both sums are taken in fp32 in a fixed order
-// (deterministic), the second about the mean so the common component does not
-// cancel precision away.  The output row must not alias the input row.
+// ns_norm.hip -- the engine's RMSNorm steps around the FFN block (metal:509-529):
+// rms / rms_half, rms_add, rms_add_then_half and its fp32 form, one workgroup
+// per row.
+#include <algorithm>
+
 #include "ns_internal.hpp"
 #include "ns_quant.hpp"
+#include "ns_rms.hpp"
 
 namespace ns {
 namespace {
@@ -37,81 +23,108 @@ __device__ __forceinline__ float block_sum(float s, float *part) {
     return tot;
 }
 
-// Rows of up to kThreads * 4 * kMaxVec values are read once into registers
-// (float4 per thread, coalesced); longer or unaligned rows take the looped path.
-constexpr int kMaxVec = 8;  // float4 loads per thread: rows of up to 8192 values
-
-template <bool HALF>
-__global__ __launch_bounds__(kThreads) void standardize_kernel(const float *__restrict__ y, uint32_t cols,
-                                                             void *__restrict__ out, bool vec_ok) {
+// The engine's RMSNorm family around the FFN block (metal:509-529; rms, rms_half,
+// rms_add, rms_add_then_half at mm:291-296, called at mm:563, :574, :576):
+//   y = (x * r) * w                                   gemma_rmsnorm[_f16]
+//   y = residual + (x * r) * w  [then * scale]        gemma_rmsnorm_add[_scale]
+//   next = (y * r2) * next_w                          ..._then_f16 (and its fp32 form)
+// with r = 1/sqrt(sum(x^2)/width + eps) per row, r2 the same over y.  One
+// workgroup per row; each thread owns the elements k = tid + j*256.  The second
+// pass re-reads y where this thread stored it, as the reference does.
+template <bool HY, bool ADD, bool THEN, bool HN>
+__global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                         const float *__restrict__ residual,
+                                                         const float *__restrict__ scale,
+                                                         const float *__restrict__ next_w, uint32_t width, float eps,
+                                                         void *y, void *__restrict__ next) {
     __shared__ float part[kThreads / 64];
-    const uint32_t t = blockIdx.x, tid = threadIdx.x;
-    const float *row = y + size_t(t) * cols;
-    const uint32_t n4 = cols / 4;
-    if (vec_ok && cols % 4 == 0 && n4 <= uint32_t(kThreads * kMaxVec)) {
-        float4 v[kMaxVec];
-        float s = 0.f;
-#pragma unroll
-        for (int i = 0; i < kMaxVec; ++i) {
-            const uint32_t j = tid + uint32_t(i) * kThreads;
-            v[i] = j < n4 ? reinterpret_cast<const float4 *>(row)[j] : float4{0.f, 0.f, 0.f, 0.f};
-            s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-        }
-        const float mean = block_sum(s, part) / float(cols);
-        float q = 0.f;
-#pragma unroll
-        for (int i = 0; i < kMaxVec; ++i) {
-            if (tid + uint32_t(i) * kThreads >= n4) continue;
-            v[i].x -= mean;
-            v[i].y -= mean;
-            v[i].z -= mean;
-            v[i].w -= mean;
-            q = __builtin_fmaf(v[i].x, v[i].x, q);
-            q = __builtin_fmaf(v[i].y, v[i].y, q);
-            q = __builtin_fmaf(v[i].z, v[i].z, q);
-            q = __builtin_fmaf(v[i].w, v[i].w, q);
-        }
-        const float var = block_sum(q, part) / float(cols);
-        const float inv = var > 0.f ? 1.0f / __builtin_sqrtf(var) : 0.f;
-#pragma unroll
-        for (int i = 0; i < kMaxVec; ++i) {
-            const uint32_t j = tid + uint32_t(i) * kThreads;
-            if (j >= n4) continue;
-            const float a = v[i].x * inv, b = v[i].y * inv, c = v[i].z * inv, d = v[i].w * inv;
-            if constexpr (HALF) {
-                typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-                reinterpret_cast<half4_t *>(out)[size_t(t) * n4 + j] = half4_t{_Float16(a), _Float16(b), _Float16(c), _Float16(d)};
-            } else {
-                reinterpret_cast<float4 *>(out)[size_t(t) * n4 + j] = float4{a, b, c, d};
-            }
-        }
-        return;
-    }
+    const size_t base = size_t(blockIdx.x) * width;
+    const uint32_t tid = threadIdx.x;
+    const float *xr = x + base;
     float s = 0.f;
-    for (uint32_t k = tid; k < cols; k += kThreads) s += row[k];
-    const float mean = block_sum(s, part) / float(cols);
-    float q = 0.f;
-    for (uint32_t k = tid; k < cols; k += kThreads) {
-        const float c = row[k] - mean;
-        q = __builtin_fmaf(c, c, q);
+    for (uint32_t k = tid; k < width; k += kThreads) s = __builtin_fmaf(xr[k], xr[k], s);
+    const float r = 1.0f / __builtin_sqrtf(block_sum(s, part) / float(width) + eps);
+    const float sc = (ADD && scale) ? *scale : 1.0f;
+    float s2 = 0.f;
+    for (uint32_t k = tid; k < width; k += kThreads) {
+        float v = (xr[k] * r) * w[k];
+        if constexpr (ADD) {
+            v = residual[base + k] + v;
+            if (scale) v *= sc;
+        }
+        if constexpr (HY) static_cast<_Float16 *>(y)[base + k] = _Float16(v);
+        else static_cast<float *>(y)[base + k] = v;
+        if constexpr (THEN) s2 = __builtin_fmaf(v, v, s2);
     }
-    const float var = block_sum(q, part) / float(cols);
-    const float inv = var > 0.f ? 1.0f / __builtin_sqrtf(var) : 0.f;
-    for (uint32_t k = tid; k < cols; k += kThreads) {
-        const float v = (row[k] - mean) * inv;
-        if constexpr (HALF) reinterpret_cast<_Float16 *>(out)[size_t(t) * cols + k] = _Float16(v);
-        else reinterpret_cast<float *>(out)[size_t(t) * cols + k] = v;
+    if constexpr (THEN) {
+        const float r2 = 1.0f / __builtin_sqrtf(block_sum(s2, part) / float(width) + eps);
+        const float *yr = static_cast<const float *>(y) + base;
+        for (uint32_t k = tid; k < width; k += kThreads) {
+            const float v = (yr[k] * r2) * next_w[k];
+            if constexpr (HN) static_cast<_Float16 *>(next)[base + k] = _Float16(v);
+            else static_cast<float *>(next)[base + k] = v;
+        }
     }
+}
+
+// The same family with the row held in registers (ns::rms_row): one memory round
+// trip per row.  HY: fp16 y (rms_half, no residual); HZ: fp16 next.
+template <bool HY, bool HZ>
+__global__ __launch_bounds__(1024) void rmsnorm_vec_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                          const float *__restrict__ residual,
+                                                          const float *__restrict__ scale,
+                                                          const float *__restrict__ next_w, uint32_t width, float eps,
+                                                          void *__restrict__ y, void *__restrict__ next) {
+    __shared__ float part[16];
+    typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+    const size_t base4 = size_t(blockIdx.x) * (width / 4);
+    auto h4 = [](const float4 &v) { return half4_t{_Float16(v.x), _Float16(v.y), _Float16(v.z), _Float16(v.w)}; };
+    rms_row<4>(reinterpret_cast<const float4 *>(x) + base4, reinterpret_cast<const float4 *>(w),
+               residual ? reinterpret_cast<const float4 *>(residual) + base4 : nullptr, scale,
+               reinterpret_cast<const float4 *>(next_w), width / 4, eps, part,
+               [&](uint32_t j, const float4 &v) {
+                   if constexpr (HY) static_cast<half4_t *>(y)[base4 + j] = h4(v);
+                   else static_cast<float4 *>(y)[base4 + j] = v;
+               },
+               [&](uint32_t j, const float4 &z) {
+                   if constexpr (HZ) static_cast<half4_t *>(next)[base4 + j] = h4(z);
+                   else static_cast<float4 *>(next)[base4 + j] = z;
+               });
 }
 
 }  // namespace
 
-hipError_t launch_standardize(const float *y, uint32_t batch, uint32_t cols, void *out, bool half,
-                              hipStream_t stream) {
-    // float4 / half4 accesses need 16-byte aligned input and output rows
-    const bool vec_ok = (reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(out)) % 16 == 0;
-    if (half) standardize_kernel<true><<<dim3(batch), dim3(kThreads), 0, stream>>>(y, cols, out, vec_ok);
-    else standardize_kernel<false><<<dim3(batch), dim3(kThreads), 0, stream>>>(y, cols, out, vec_ok);
+hipError_t launch_rmsnorm(const float *x, const float *w, const float *residual, const float *scale,
+                          const float *next_w, uint32_t rows, uint32_t width, float eps, void *y, bool half_y,
+                          void *next, bool half_next, hipStream_t stream) {
+    if (next_w && !residual) return hipErrorInvalidValue;  // the second norm follows rms_add only
+    if (residual && half_y) return hipErrorInvalidValue;   // rms_add writes the fp32 residual stream
+    const dim3 g(rows);
+    // The register form: rows of up to 4 float4 per thread at up to 1024 threads, 16-byte
+    // aligned (fp16 outputs 8-byte aligned).
+    auto al = [](const void *p, uintptr_t a) { return !p || reinterpret_cast<uintptr_t>(p) % a == 0; };
+    const uint32_t n4 = width / 4;
+    const bool vec = width % 4 == 0 && n4 <= 4096 && al(x, 16) && al(w, 16) && al(residual, 16) &&
+                     al(next_w, 16) && al(y, half_y ? 8 : 16) && al(next, half_next ? 8 : 16);
+    if (vec) {
+        const uint32_t nt = std::min(1024u, std::max(64u, ((n4 + 3) / 4 + 63) / 64 * 64));
+        const dim3 b(nt);
+        if (half_y) rmsnorm_vec_kernel<true, false><<<g, b, 0, stream>>>(x, w, nullptr, nullptr, nullptr, width, eps, y, nullptr);
+        else if (half_next) rmsnorm_vec_kernel<false, true><<<g, b, 0, stream>>>(x, w, residual, scale, next_w, width, eps, y, next);
+        else rmsnorm_vec_kernel<false, false><<<g, b, 0, stream>>>(x, w, residual, scale, next_w, width, eps, y, next);
+        return hipGetLastError();
+    }
+    const dim3 b(kThreads);
+    if (!residual) {
+        if (half_y) rmsnorm_kernel<true, false, false, false><<<g, b, 0, stream>>>(x, w, nullptr, nullptr, nullptr, width, eps, y, nullptr);
+        else rmsnorm_kernel<false, false, false, false><<<g, b, 0, stream>>>(x, w, nullptr, nullptr, nullptr, width, eps, y, nullptr);
+    } else if (!next_w) {
+        rmsnorm_kernel<false, true, false, false><<<g, b, 0, stream>>>(x, w, residual, scale, nullptr, width, eps, y, nullptr);
+    } else if (half_next) {
+        rmsnorm_kernel<false, true, true, true><<<g, b, 0, stream>>>(x, w, residual, scale, next_w, width, eps, y, next);
+    } else {
+        rmsnorm_kernel<false, true, true, false><<<g, b, 0, stream>>>(x, w, residual, scale, next_w, width, eps, y, next);
+    }
     return hipGetLastError();
 }
 

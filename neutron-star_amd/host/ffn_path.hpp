@@ -166,10 +166,35 @@ public:
         ffn_down(e, down, mid, out, batch, prefill, fast_swa);
     }
 
-    // Inter-layer step of the FFN stack: out = (y - mean) / rms(y - mean) per
-    // token, fp16 (half_out) or fp32; y fp32 [batch][cols].
-    void standardize(hipStream_t e, const float *y, uint32_t batch, uint32_t cols, void *out, bool half_out) const {
-        check(ns_standardize(ctx_, y, batch, cols, out, half_out ? 1 : 0, e));
+    // The RMSNorm helpers around the FFN block (mm:291-296; metal:509-529).  Norm
+    // weights are fp32 device vectors of `width`; eps is the model's epsilon.
+    // rms (mm:291): out = (in * r) * w per row, r = 1/sqrt(mean(in^2) + eps).
+    void rms(hipStream_t e, const float *in, float *out, const float *w, uint32_t width, uint32_t rows,
+             float eps) const {
+        check(ns_rmsnorm(ctx_, in, w, rows, width, eps, out, 0, e));
+    }
+    // rms_half (mm:292): the same into fp16 (the engine's halfbuf).
+    void rms_half(hipStream_t e, const float *in, const float *w, uint32_t width, uint32_t rows, float eps,
+                  uint16_t *half_out) const {
+        check(ns_rmsnorm(ctx_, in, w, rows, width, eps, half_out, 1, e));
+    }
+    // rms_add (mm:295): out = residual + (in * r) * w, times *scale when given.
+    void rms_add(hipStream_t e, const float *in, const float *residual, float *out, const float *w, uint32_t width,
+                 uint32_t rows, float eps, const float *scale = nullptr) const {
+        check(ns_rmsnorm_add(ctx_, in, w, residual, scale, rows, width, eps, out, e));
+    }
+    // rms_add_then_half (mm:296): rms_add into `out`, then half((out * r2) * next_w).
+    void rms_add_then_half(hipStream_t e, const float *in, const float *residual, float *out, const float *w,
+                           const float *next_w, uint32_t width, uint32_t rows, float eps, uint16_t *half_out,
+                           const float *scale = nullptr) const {
+        check(ns_rmsnorm_add_then(ctx_, in, w, residual, scale, next_w, rows, width, eps, out, half_out, 1, e));
+    }
+    // rms (mm:563, decode) fused into gate_up_geglu_decode (mm:571): one launch.
+    void rms_gate_up_geglu_decode(hipStream_t e, const Tensor &gate, const Tensor &up, const float *in,
+                                  const float *norm_w, float eps, float *out) const {
+        same_shape(gate, up);
+        check(ns_rms_gate_up_geglu_decode(ctx_, w_.data(gate), w_.data(up), int(w_.layout(gate)), cols(gate),
+                                          rows(gate), in, norm_w, eps, out, e));
     }
 
 private:

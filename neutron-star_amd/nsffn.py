@@ -65,7 +65,10 @@ def lib():
             "ns_gate_up_geglu": [vp, vp, vp, i32, u32, u32, u32, vp, vp, vp],
             "ns_ffn_down": [vp, vp, i32, i32, u32, u32, u32, vp, i32, i32, vp, vp],
             "ns_dequant": [vp, vp, i32, i32, u32, u32, u32, u32, vp, vp, vp],
-            "ns_standardize": [vp, vp, u32, u32, vp, i32, vp],
+            "ns_rmsnorm": [vp, vp, vp, u32, u32, ctypes.c_float, vp, i32, vp],
+            "ns_rmsnorm_add": [vp, vp, vp, vp, vp, u32, u32, ctypes.c_float, vp, vp],
+            "ns_rmsnorm_add_then": [vp, vp, vp, vp, vp, vp, u32, u32, ctypes.c_float, vp, vp, i32, vp],
+            "ns_rms_gate_up_geglu_decode": [vp, vp, vp, i32, u32, u32, vp, vp, ctypes.c_float, vp, vp],
             "ns_retile": [vp, vp, i32, u32, u32, i32, i32],
             "ns_retile_device": [vp, vp, i32, u32, u32, i32, i32, vp],
             "ns_synth_blocks": [i32, u64, u64, u64, vp, i32],
@@ -260,9 +263,27 @@ class Context:
                                           else inp, mid[t * ffn:(t + 1) * ffn] if batch > 1 else mid, stream)
         self.ffn_down(down, down_type, layout, ffn, cols, batch, mid, out, prefill, fast, stream)
 
-    def standardize(self, y, batch, cols, out, out_half, stream=None):
-        """Config 4's inter-layer step: out = (y - mean) / rms(y - mean) per token."""
-        check(lib().ns_standardize(self.handle, _ptr(y), batch, cols, _ptr(out), int(out_half), _stream(stream)))
+    def rmsnorm(self, x, weight, rows, width, eps, y, half_out=False, stream=None):
+        """rms / rms_half (mm:291-292): y = (x * r) * weight per row."""
+        check(lib().ns_rmsnorm(self.handle, _ptr(x), _ptr(weight), rows, width, eps, _ptr(y), int(half_out),
+                               _stream(stream)))
+
+    def rmsnorm_add(self, x, weight, residual, scale, rows, width, eps, y, stream=None):
+        """rms_add (mm:295): y = residual + (x * r) * weight [* scale]."""
+        check(lib().ns_rmsnorm_add(self.handle, _ptr(x), _ptr(weight), _ptr(residual), _ptr(scale), rows, width,
+                                   eps, _ptr(y), _stream(stream)))
+
+    def rmsnorm_add_then(self, x, weight, residual, scale, next_weight, rows, width, eps, y, nxt, half_next,
+                         stream=None):
+        """rms_add_then_half (mm:296) or, with half_next False, rms_add followed by rms."""
+        check(lib().ns_rmsnorm_add_then(self.handle, _ptr(x), _ptr(weight), _ptr(residual), _ptr(scale),
+                                        _ptr(next_weight), rows, width, eps, _ptr(y), _ptr(nxt), int(half_next),
+                                        _stream(stream)))
+
+    def rms_gate_up_geglu_decode(self, wg, wu, layout, cols, rows, x, norm_weight, eps, h, stream=None):
+        """rms (mm:563) then gate_up_geglu_decode (mm:571), one launch."""
+        check(lib().ns_rms_gate_up_geglu_decode(self.handle, _ptr(wg), _ptr(wu), layout, cols, rows, _ptr(x),
+                                                _ptr(norm_weight), eps, _ptr(h), _stream(stream)))
 
     def dequant(self, w, qtype, layout, cols, rows, row0, nrows, out_f32=None, out_f16=None, stream=None):
         check(lib().ns_dequant(self.handle, _ptr(w), qtype, layout, cols, rows, row0, nrows,

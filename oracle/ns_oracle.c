@@ -159,6 +159,41 @@ float nso_gelu_tanh(float g) {
     return 0.5f * g * (1.0f + tanhf(0.7978845608028654f * g * (1.0f + 0.044715f * g * g)));
 }
 
+/* metal/gemma4.metal:509-529, the RMSNorm family the engine runs around the FFN block
+ * (rms, rms_half, rms_add, rms_add_then_half: metal_engine.mm:291-296).  Per row:
+ *   s = sum_k x[k]*x[k] (sequential), r = 1/sqrtf(s/width + eps)          (metal:510, :517)
+ *   y[k] = (x[k]*r)*w[k], plus residual[k] first when residual != NULL,
+ *          times *scale when scale != NULL                                (metal:511, :517, :520)
+ *   with next_w: s2 over y, next[k] = (y[k]*r2)*next_w[k]                  (metal:524-525)
+ * The reference sums in 256-thread strides plus simd_sum (metal:510); this is the
+ * sequential order, so outputs agree to rounding. */
+int nso_rmsnorm(const float *x, const float *w, const float *residual, const float *scale, const float *next_w,
+                uint64_t rows, uint64_t width, float eps, float *y, float *next) {
+    if (width == 0 || (next_w && !next)) return -1;
+    for (uint64_t t = 0; t < rows; ++t) {
+        const float *xr = x + t * width;
+        float *yr = y + t * width;
+        float s = 0.0f;
+        for (uint64_t k = 0; k < width; ++k) s += xr[k] * xr[k];
+        const float r = 1.0f / sqrtf(s / (float)width + eps);
+        float s2 = 0.0f;
+        for (uint64_t k = 0; k < width; ++k) {
+            float v = (xr[k] * r) * w[k];
+            if (residual) {
+                v = residual[t * width + k] + v;
+                if (scale) v *= *scale;
+            }
+            yr[k] = v;
+            s2 += v * v;
+        }
+        if (next_w) {
+            const float r2 = 1.0f / sqrtf(s2 / (float)width + eps);
+            for (uint64_t k = 0; k < width; ++k) next[t * width + k] = (yr[k] * r2) * next_w[k];
+        }
+    }
+    return 0;
+}
+
 /* ---- threaded drivers ---------------------------------------------------- */
 
 typedef struct {

@@ -63,6 +63,12 @@ int nso_gemv(int type, int layout, const uint8_t *w, uint64_t cols, uint64_t row
 
 float nso_gelu_tanh(float g);
 
+/* The RMSNorm family (metal:509-529): y = [residual +] (x*r)*w [* *scale], and with
+ * next_w also next = (y*r2)*next_w; r = 1/sqrtf(mean(x^2) + eps), r2 likewise over y.
+ * residual, scale, next_w (with next) may be NULL.  x, y: [rows][width]. */
+int nso_rmsnorm(const float *x, const float *w, const float *residual, const float *scale, const float *next_w,
+                uint64_t rows, uint64_t width, float eps, float *y, float *next);
+
 /* h = gelu_tanh(Wg x) * (Wu x), fp32 (decode regime, always FP32). */
 int nso_gate_up_geglu(int layout, const uint8_t *wg, const uint8_t *wu, uint64_t cols,
                       uint64_t rows, const float *x, float *h, int nthreads);

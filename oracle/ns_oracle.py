@@ -47,6 +47,7 @@ def lib():
         L.nso_gate_up_geglu.argtypes = [i32, vp, vp, u64, u64, vp, vp, i32]
         L.nso_gemm.argtypes = [i32, i32, vp, u64, u64, u64, vp, i32, vp, i32]
         L.nso_gate_up_geglu_prefill.argtypes = [i32, vp, vp, u64, u64, u64, vp, i32, vp, i32]
+        L.nso_rmsnorm.argtypes = [vp, vp, vp, vp, vp, u64, u64, f32, vp, vp]
         _lib = L
     return _lib
 
@@ -64,7 +65,7 @@ def ref():
 
 
 def _p(a):
-    return a.ctypes.data
+    return None if a is None else a.ctypes.data
 
 
 def _nt(n):
@@ -117,6 +118,25 @@ def gate_up_geglu_prefill(layout, wg, wu, cols, rows, batch, x_f16, acc_mode, nt
 
 def gelu_tanh(g):
     return lib().nso_gelu_tanh(g)
+
+
+def rmsnorm(x, w, residual=None, scale=None, next_w=None, eps=1e-6):
+    """metal:509-529 per row of x ([rows][width] or [width]): returns y, or (y, next) with next_w.
+    scale is a Python float (the reference reads it from a one-float tensor)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    shape = x.shape
+    x2 = x.reshape(-1, shape[-1])
+    rows, width = x2.shape
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    res = None if residual is None else np.ascontiguousarray(residual, dtype=np.float32).reshape(rows, width)
+    sc = None if scale is None else np.array([scale], dtype=np.float32)
+    nw = None if next_w is None else np.ascontiguousarray(next_w, dtype=np.float32)
+    y = np.empty((rows, width), dtype=np.float32)
+    nxt = np.empty((rows, width), dtype=np.float32) if nw is not None else None
+    assert lib().nso_rmsnorm(_p(x2), _p(w), _p(res), _p(sc), _p(nw), rows, width, eps, _p(y), _p(nxt)) == 0
+    if nw is None:
+        return y.reshape(shape)
+    return y.reshape(shape), nxt.reshape(shape)
 
 
 def ref_dequant(qtype, w, cols, rows, first, count):

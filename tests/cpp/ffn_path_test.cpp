@@ -188,17 +188,25 @@ int main() {
                         true, s);
         }
         FfnPath p2(img2);
-        // decode block (always FP32) + standardised rescale
+        // decode block (always FP32), then the next layer's RMSNorm (rms, mm:563) with unit
+        // weights: unit RMS; and rms fused into the next gate/up equals rms then gate/up
         float *dx2 = dev(std::vector<float>(D));
+        float *dones = dev(std::vector<float>(D, 1.0f));
+        float *dh2 = dev(std::vector<float>(F));
+        float *dh3 = dev(std::vector<float>(F));
         p2.ffn_block(s, g2, u2, d2, dx, dh, dy, 1, /*prefill=*/false, /*swa=*/true, /*exact_ffn=*/false);
-        p2.standardize(s, dy, 1, uint32_t(D), dx2, false);
+        p2.rms(s, dy, dx2, dones, uint32_t(D), 1, 0.0f);
+        p2.gate_up_geglu_decode(s, g2, u2, dx2, dh2);
+        p2.rms_gate_up_geglu_decode(s, g2, u2, dy, dones, 0.0f, dh3);
         if (hipStreamSynchronize(s) != hipSuccess) return 3;
         const auto yb = host(dy, D), xr = host(dx2, D);
         expect(rel_err(yb, y_ref, 1, D) <= 1e-3 && rel_err(host(dh, F), h_ref, 1, F) <= 1e-3,
                "ffn_block decode from the .nsmffn file within 1e-3");
         double ss = 0;
         for (float v : xr) ss += double(v) * v;
-        expect(std::fabs(std::sqrt(ss / D) - 1.0) < 1e-5, "standardize output has unit RMS");
+        expect(std::fabs(std::sqrt(ss / D) - 1.0) < 1e-5, "rms with unit weights: unit RMS");
+        expect(rel_err(host(dh3, F), host(dh2, F), 1, F) <= 1e-5, "rms fused into gate/up == rms then gate/up");
+        (void)hipFree(dones); (void)hipFree(dh2); (void)hipFree(dh3);
         // prefill block: a local (swa) layer runs FP16 mode, a global one or --exact-ffn FP32 (mm:565)
         for (int c = 0; c < 3; ++c) {
             const bool swa = c != 1, exact = c == 2;

@@ -224,3 +224,50 @@ def test_round_f16p():
     r = L.nso_round_f16p(float(big))
     assert np.isfinite(r) and abs(r - big) <= big * 2.0**-11
     assert L.nso_round_f16p(1.0 + 2.0**-11) == 1.0 and L.nso_round_f16p(1.0 + 3 * 2.0**-11) == 1.0 + 2.0**-9
+
+
+# ---- the RMSNorm family (metal:509-529) ---------------------------------------------
+
+def test_rmsnorm_known_answers():
+    """Closed forms: x = (3, 4, 0, 0) has mean square 25/4, so r = 0.4 exactly with eps = 0;
+    a constant row c has r = 1/sqrt(c^2 + eps); a zero row with eps > 0 maps to zeros."""
+    w = np.array([1.0, 2.0, -1.0, 0.5], dtype=np.float32)
+    y = O.rmsnorm(np.array([3.0, 4.0, 0.0, 0.0], dtype=np.float32), w, eps=0.0)
+    np.testing.assert_array_equal(y, np.float32([1.2, 3.2, 0.0, 0.0]))
+    c, eps = np.float32(-2.5), np.float32(1e-3)
+    y = O.rmsnorm(np.full(64, c, dtype=np.float32), np.ones(64, dtype=np.float32), eps=float(eps))
+    expect = float(c) / np.sqrt(float(c) ** 2 + float(eps))
+    assert np.allclose(y, expect, rtol=2e-7, atol=0)
+    assert not np.any(O.rmsnorm(np.zeros(16, np.float32), np.ones(16, np.float32), eps=1e-6))
+
+
+def test_rmsnorm_unit_rms_and_scale_invariance():
+    """With w = 1 and eps = 0 the output has mean square 1; scaling x by 2^k leaves the
+    output unchanged bit for bit (the sum scales by 4^k exactly, the root by 2^k)."""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((3, 3840)).astype(np.float32)
+    ones = np.ones(3840, dtype=np.float32)
+    y = O.rmsnorm(x, ones, eps=0.0)
+    assert np.allclose(np.mean(y.astype(np.float64) ** 2, axis=1), 1.0, rtol=1e-5)
+    w = rng.standard_normal(3840).astype(np.float32)
+    for k in (-6, 3, 10):
+        np.testing.assert_array_equal(O.rmsnorm(x * np.float32(2.0 ** k), w, eps=0.0), O.rmsnorm(x, w, eps=0.0))
+
+
+def test_rmsnorm_add_and_then():
+    """rms_add: a zero input with eps > 0 returns the residual (times scale) exactly; the
+    residual enters additively.  The _then form equals rms_add followed by rms (mm:563)."""
+    rng = np.random.default_rng(6)
+    res = rng.standard_normal(256).astype(np.float32)
+    w = rng.standard_normal(256).astype(np.float32)
+    np.testing.assert_array_equal(O.rmsnorm(np.zeros(256, np.float32), w, residual=res, eps=1e-6), res)
+    np.testing.assert_array_equal(O.rmsnorm(np.zeros(256, np.float32), w, residual=res, scale=0.5, eps=1e-6),
+                                  res * np.float32(0.5))
+    x = rng.standard_normal(256).astype(np.float32)
+    y0 = O.rmsnorm(x, w, eps=1e-6)
+    y1 = O.rmsnorm(x, w, residual=np.zeros(256, np.float32), eps=1e-6)
+    np.testing.assert_array_equal(y1, y0)  # 0 + v == v
+    nw = rng.standard_normal(256).astype(np.float32)
+    y, nxt = O.rmsnorm(x, w, residual=res, scale=0.75, next_w=nw, eps=1e-6)
+    np.testing.assert_array_equal(y, O.rmsnorm(x, w, residual=res, scale=0.75, eps=1e-6))
+    np.testing.assert_array_equal(nxt, O.rmsnorm(y, nw, eps=1e-6))
