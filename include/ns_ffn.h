@@ -217,6 +217,48 @@ uint64_t ns_nsmffn_size(const ns_nsmffn *f);    /* MetalFfnFile::file_size */
 /* MetalFfnFile::offset and ::reordered of the tensor whose GGUF offset is source_offset. */
 int ns_nsmffn_lookup(const ns_nsmffn *f, uint64_t source_offset, uint64_t *offset, int *reordered);
 
+/* ---- GGUF v3 reader (host side; no GPU needed) ----------------------------------------------
+ * The engine's GGUF class (gguf.cpp:71-129, gguf.hpp:29-60): ns_gguf_open mmaps `path`
+ * read-only and parses the header, metadata and tensor table with the reference's checks and
+ * messages (NS_ERR_FORMAT: "bad GGUF magic", "only GGUF v3 is supported", "truncated GGUF
+ * header", "invalid GGUF counts", "invalid tensor rank", "invalid quantized tensor shape: <name>",
+ * "unsupported tensor type <id>: <name>", "tensor outside GGUF mapping: <name>", ...).  The data
+ * section starts at the header's end rounded up to general.alignment (default 32).  prefetch != 0
+ * asks the kernel to page the file in (skipped when NEUTRON_NO_SSD_PREFETCH is set). */
+typedef struct ns_gguf ns_gguf;
+typedef struct ns_gguf_tensor_info {
+    const char *name; /* owned by the ns_gguf */
+    uint32_t type;    /* GGUF type id: 0 F32, 1 F16, 12 Q4_K, 14 Q6_K */
+    uint32_t n_dims;
+    uint64_t shape[4];
+    uint64_t offset; /* Tensor::offset, from the data section */
+    uint64_t bytes;  /* Tensor::bytes */
+} ns_gguf_tensor_info;
+
+int ns_gguf_open(const char *path, int prefetch, ns_gguf **out);
+int ns_gguf_close(ns_gguf *g);
+uint64_t ns_gguf_data_offset(const ns_gguf *g);   /* GGUF::data_offset */
+uint64_t ns_gguf_file_size(const ns_gguf *g);     /* GGUF::file_size */
+const void *ns_gguf_mapped_data(const ns_gguf *g); /* GGUF::mapped_data */
+uint32_t ns_gguf_tensor_count(const ns_gguf *g);  /* GGUF::tensors().size() */
+int ns_gguf_tensor(const ns_gguf *g, uint32_t index, ns_gguf_tensor_info *out);
+/* GGUF::tensor(name) / has_tensor: "missing tensor: <name>" when absent. */
+int ns_gguf_find_tensor(const ns_gguf *g, const char *name, uint32_t *index);
+/* GGUF::has, meta_u64 (integers of any width and sign), meta_number (integers or floats),
+ * meta<std::string>, and typed arrays (element type as the GGUF value type; data is NULL for
+ * string arrays).  "missing GGUF metadata: <key>" / "metadata is not integer: <key>". */
+int ns_gguf_has_meta(const ns_gguf *g, const char *key);
+int ns_gguf_meta_u64(const ns_gguf *g, const char *key, uint64_t *out);
+int ns_gguf_meta_number(const ns_gguf *g, const char *key, double *out);
+int ns_gguf_meta_string(const ns_gguf *g, const char *key, const char **out);
+int ns_gguf_meta_array(const ns_gguf *g, const char *key, uint32_t *elem_type, uint64_t *count,
+                       const void **data);
+/* The tensor table for the .nsmffn functions, in GGUF order: each FFN matrix
+ * (blk.<i>.ffn_gate / ffn_up / ffn_down.weight, the Gemma4Model names at model.cpp:17) gets its
+ * layer and kind, as ffn_tensors() assigns them (metal_ffn.cpp:63-71); every other tensor
+ * NS_FFN_NONE.  With out == NULL only *count is set. */
+int ns_gguf_ffn_table(const ns_gguf *g, ns_tensor_desc *out, uint32_t capacity, uint32_t *count);
+
 #ifdef __cplusplus
 }
 #endif

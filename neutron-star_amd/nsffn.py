@@ -55,6 +55,10 @@ def lib():
         L.ns_nsmffn_data.argtypes = [vp]
         L.ns_nsmffn_size.restype = u64
         L.ns_nsmffn_size.argtypes = [vp]
+        for name, rt in (("ns_gguf_data_offset", u64), ("ns_gguf_file_size", u64), ("ns_gguf_mapped_data", vp),
+                         ("ns_gguf_tensor_count", u32)):
+            getattr(L, name).restype = rt
+            getattr(L, name).argtypes = [vp]
         sigs = {
             "ns_abi_version": [],
             "ns_ctx_create": [i32, ctypes.POINTER(vp)],
@@ -79,6 +83,17 @@ def lib():
             "ns_nsmffn_open": [ctypes.c_char_p, u64, u64, vp, u32, ctypes.POINTER(vp)],
             "ns_nsmffn_close": [vp],
             "ns_nsmffn_lookup": [vp, u64, ctypes.POINTER(u64), ctypes.POINTER(i32)],
+            "ns_gguf_open": [ctypes.c_char_p, i32, ctypes.POINTER(vp)],
+            "ns_gguf_close": [vp],
+            "ns_gguf_tensor": [vp, u32, ctypes.POINTER(GgufTensorInfo)],
+            "ns_gguf_find_tensor": [vp, ctypes.c_char_p, ctypes.POINTER(u32)],
+            "ns_gguf_has_meta": [vp, ctypes.c_char_p],
+            "ns_gguf_meta_u64": [vp, ctypes.c_char_p, ctypes.POINTER(u64)],
+            "ns_gguf_meta_number": [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)],
+            "ns_gguf_meta_string": [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p)],
+            "ns_gguf_meta_array": [vp, ctypes.c_char_p, ctypes.POINTER(u32), ctypes.POINTER(u64),
+                                   ctypes.POINTER(vp)],
+            "ns_gguf_ffn_table": [vp, vp, u32, ctypes.POINTER(u32)],
         }
         for name, args in sigs.items():
             f = getattr(L, name)
@@ -206,6 +221,98 @@ class NsmffnFile:
     def view(self, offset, nbytes):
         """Bytes [offset, offset + nbytes) of the mapping (a copy)."""
         base = lib().ns_nsmffn_data(self.handle)
+        return np.frombuffer((ctypes.c_uint8 * nbytes).from_address(base + offset), dtype=np.uint8).copy()
+
+
+# ---- GGUF v3 reader -----------------------------------------------------------
+
+class GgufTensorInfo(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("type", ctypes.c_uint32), ("n_dims", ctypes.c_uint32),
+                ("shape", ctypes.c_uint64 * 4), ("offset", ctypes.c_uint64), ("bytes", ctypes.c_uint64)]
+
+
+# numpy element type of each GGUF array value type
+GGUF_ARRAY_DTYPES = {0: np.uint8, 1: np.int8, 2: np.uint16, 3: np.int16, 4: np.uint32, 5: np.int32,
+                     6: np.float32, 7: np.uint8, 10: np.uint64, 11: np.int64, 12: np.float64}
+
+
+class GgufFile:
+    """GGUF (src/native/gguf.cpp:71-129): a validated read-only mapping of a GGUF v3 file."""
+
+    handle = None
+
+    def __init__(self, path, prefetch=False):
+        h = ctypes.c_void_p()
+        check(lib().ns_gguf_open(str(path).encode(), int(prefetch), ctypes.byref(h)))
+        self.handle = h
+
+    def close(self):
+        if self.handle:
+            lib().ns_gguf_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
+
+    def data_offset(self):
+        return lib().ns_gguf_data_offset(self.handle)
+
+    def file_size(self):
+        return lib().ns_gguf_file_size(self.handle)
+
+    def tensors(self):
+        """[(name, type, shape, offset, bytes)] in GGUF order."""
+        out = []
+        for i in range(lib().ns_gguf_tensor_count(self.handle)):
+            t = GgufTensorInfo()
+            check(lib().ns_gguf_tensor(self.handle, i, ctypes.byref(t)))
+            out.append((t.name.decode(), t.type, tuple(t.shape[:t.n_dims]), t.offset, t.bytes))
+        return out
+
+    def find(self, name):
+        idx = ctypes.c_uint32()
+        check(lib().ns_gguf_find_tensor(self.handle, name.encode(), ctypes.byref(idx)))
+        return idx.value
+
+    def has(self, key):
+        return bool(lib().ns_gguf_has_meta(self.handle, key.encode()))
+
+    def meta_u64(self, key):
+        v = ctypes.c_uint64()
+        check(lib().ns_gguf_meta_u64(self.handle, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def meta_number(self, key):
+        v = ctypes.c_double()
+        check(lib().ns_gguf_meta_number(self.handle, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def meta_string(self, key):
+        v = ctypes.c_char_p()
+        check(lib().ns_gguf_meta_string(self.handle, key.encode(), ctypes.byref(v)))
+        return v.value.decode()
+
+    def meta_array(self, key):
+        """(element type, numpy array or None for string arrays, count)."""
+        et, n, p = ctypes.c_uint32(), ctypes.c_uint64(), ctypes.c_void_p()
+        check(lib().ns_gguf_meta_array(self.handle, key.encode(), ctypes.byref(et), ctypes.byref(n),
+                                       ctypes.byref(p)))
+        if et.value == 8:
+            return et.value, None, n.value
+        dt = np.dtype(GGUF_ARRAY_DTYPES[et.value])
+        raw = (ctypes.c_uint8 * (n.value * dt.itemsize)).from_address(p.value) if n.value else b""
+        return et.value, np.frombuffer(bytes(raw), dtype=dt), n.value
+
+    def ffn_table(self):
+        """The ns_tensor_desc table for the .nsmffn functions (ffn_tensors, metal_ffn.cpp:63-71)."""
+        n = ctypes.c_uint32()
+        check(lib().ns_gguf_ffn_table(self.handle, None, 0, ctypes.byref(n)))
+        table = np.zeros(n.value, dtype=TENSOR_DESC)
+        check(lib().ns_gguf_ffn_table(self.handle, _ptr(table), n.value, ctypes.byref(n)))
+        return table
+
+    def bytes_at(self, offset, nbytes):
+        base = lib().ns_gguf_mapped_data(self.handle)
         return np.frombuffer((ctypes.c_uint8 * nbytes).from_address(base + offset), dtype=np.uint8).copy()
 
 

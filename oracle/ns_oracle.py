@@ -11,6 +11,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libns_oracle.so")
 REF_PATH = os.path.join(HERE, "_ref", "libns_ref_quant.so")
+REF_GGUF_PATH = os.path.join(HERE, "_ref", "libns_ref_gguf.so")
 
 Q4_K, Q6_K = 12, 14
 ROW_MAJOR, NSMFFN = 0, 1
@@ -150,3 +151,99 @@ def ref_dot_row(qtype, w, cols, rows, row, x):
     out = np.zeros(1, dtype=np.float32)
     rc = ref().nsref_dot_row(qtype, _p(w), cols, rows, row, _p(x), _p(out))
     return rc, out[0]
+
+
+# ---- the reference's own GGUF reader (oracle/_ref/libns_ref_gguf.so) -------------
+
+_ref_gguf = None
+
+
+def ref_gguf_available():
+    return os.path.exists(REF_GGUF_PATH)
+
+
+def ref_gguf():
+    global _ref_gguf
+    if _ref_gguf is None:
+        R = ctypes.CDLL(REF_GGUF_PATH)
+        vp, u32, u64, cp = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_char_p
+        R.nsref_gguf_open.restype = vp
+        R.nsref_gguf_open.argtypes = [cp, vp, u64]
+        R.nsref_gguf_close.argtypes = [vp]
+        for n in ("nsref_gguf_data_offset", "nsref_gguf_file_size"):
+            getattr(R, n).restype = u64
+            getattr(R, n).argtypes = [vp]
+        R.nsref_gguf_tensor_count.restype = u32
+        R.nsref_gguf_tensor_count.argtypes = [vp]
+        R.nsref_gguf_tensor.argtypes = [vp, u32, vp, u64, vp, vp, vp, vp, vp]
+        R.nsref_gguf_find.argtypes = [vp, cp, vp, u64]
+        R.nsref_gguf_meta_u64.argtypes = [vp, cp, vp, vp, u64]
+        R.nsref_gguf_meta_number.argtypes = [vp, cp, vp, vp, u64]
+        R.nsref_gguf_meta_string.argtypes = [vp, cp, vp, u64]
+        R.nsref_gguf_meta_array.argtypes = [vp, cp, ctypes.c_int, vp, u64, vp]
+        _ref_gguf = R
+    return _ref_gguf
+
+
+class RefGguf:
+    """The reference's GGUF class on a file: .error is its exception message when the
+    constructor threw, else the parsed fields are available."""
+
+    def __init__(self, path):
+        err = ctypes.create_string_buffer(512)
+        self.h = ref_gguf().nsref_gguf_open(str(path).encode(), err, 512)
+        self.error = None if self.h else err.value.decode()
+
+    def close(self):
+        if self.h:
+            ref_gguf().nsref_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def data_offset(self):
+        return ref_gguf().nsref_gguf_data_offset(self.h)
+
+    def file_size(self):
+        return ref_gguf().nsref_gguf_file_size(self.h)
+
+    def tensors(self):
+        out = []
+        for i in range(ref_gguf().nsref_gguf_tensor_count(self.h)):
+            name = ctypes.create_string_buffer(1024)
+            t, nd, off, nb = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint64(), ctypes.c_uint64()
+            shape = (ctypes.c_uint64 * 4)()
+            ref_gguf().nsref_gguf_tensor(self.h, i, name, 1024, ctypes.byref(t), ctypes.byref(nd), shape,
+                                         ctypes.byref(off), ctypes.byref(nb))
+            out.append((name.value.decode(), t.value, tuple(shape[:nd.value]), off.value, nb.value))
+        return out
+
+    def find(self, name):
+        err = ctypes.create_string_buffer(512)
+        rc = ref_gguf().nsref_gguf_find(self.h, name.encode(), err, 512)
+        return None if rc == 0 else err.value.decode()
+
+    def meta_u64(self, key):
+        v, err = ctypes.c_uint64(), ctypes.create_string_buffer(512)
+        rc = ref_gguf().nsref_gguf_meta_u64(self.h, key.encode(), ctypes.byref(v), err, 512)
+        return (v.value, None) if rc == 0 else (None, err.value.decode())
+
+    def meta_number(self, key):
+        v, err = ctypes.c_double(), ctypes.create_string_buffer(512)
+        rc = ref_gguf().nsref_gguf_meta_number(self.h, key.encode(), ctypes.byref(v), err, 512)
+        return (v.value, None) if rc == 0 else (None, err.value.decode())
+
+    def meta_string(self, key):
+        out = ctypes.create_string_buffer(1 << 16)
+        rc = ref_gguf().nsref_gguf_meta_string(self.h, key.encode(), out, 1 << 16)
+        return (out.value.decode(), None) if rc == 0 else (None, out.value.decode())
+
+    def meta_array(self, key, elem, dtype):
+        cap = 1 << 20
+        buf = ctypes.create_string_buffer(cap)
+        n = ctypes.c_uint64()
+        rc = ref_gguf().nsref_gguf_meta_array(self.h, key.encode(), elem, buf, cap, ctypes.byref(n))
+        if rc:
+            return None
+        return np.frombuffer(buf.raw[:n.value * np.dtype(dtype).itemsize], dtype=dtype)

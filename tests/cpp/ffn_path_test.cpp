@@ -16,6 +16,7 @@
 #include <unistd.h>
 
 #include "ffn_path.hpp"
+#include "gguf_file.hpp"
 #include "nsmffn_file.hpp"
 #include "ns_oracle.h"
 
@@ -152,9 +153,8 @@ int main() {
     try { path.matmul(s, gate, dx, dh, 0); } catch (const std::runtime_error &e) { threw = std::strstr(e.what(), "batch") != nullptr; }
     expect(threw, "zero batch throws with the C ABI message");
 
-    // ---- load chain: GGUF image -> .nsmffn -> MetalFfnFile -> WeightImage -> ffn_block
+    // ---- load chain: GGUF v3 file -> GGUF -> .nsmffn -> MetalFfnFile -> WeightImage -> ffn_block
     {
-        const uint64_t data_offset = 65536 + 512;
         const Tensor *ts[4] = {&gate, &up, &down, &embd};
         const std::vector<uint8_t> *hs[4] = {&hg, &hu, &hd, &he};
         std::vector<ns_tensor_desc> table;
@@ -166,12 +166,50 @@ int main() {
                              ffn ? 0u : NS_FFN_NONE, ffn ? uint32_t(i) : NS_FFN_NONE, 0});
             pos += (t.bytes + 31) / 32 * 32;
         }
-        std::vector<uint8_t> gguf(data_offset + pos, 0);
-        for (size_t i = 0; i < data_offset; ++i) gguf[i] = uint8_t(i * 131 + 7);  // stand-in metadata bytes
+        // GGUF v3 header: one metadata entry (general.alignment = 65536, so the data section
+        // starts past the .nsmffn header page) and the four tensor entries
+        std::vector<uint8_t> gguf;
+        auto put = [&](const void *p, size_t n) {
+            gguf.insert(gguf.end(), static_cast<const uint8_t *>(p), static_cast<const uint8_t *>(p) + n);
+        };
+        auto put32 = [&](uint32_t v) { put(&v, 4); };
+        auto put64 = [&](uint64_t v) { put(&v, 8); };
+        auto putstr = [&](const std::string &s) { put64(s.size()); put(s.data(), s.size()); };
+        put("GGUF", 4); put32(3); put64(4); put64(1);
+        putstr("general.alignment"); put32(4 /* u32 */); put32(65536);
+        for (int i = 0; i < 4; ++i) {
+            putstr(ts[i]->name); put32(2); put64(ts[i]->shape[0]); put64(ts[i]->shape[1]);
+            put32(uint32_t(ts[i]->type)); put64(table[i].source_offset);
+        }
+        const uint64_t data_offset = 65536;
+        for (size_t i = gguf.size(); i < data_offset; ++i) gguf.push_back(uint8_t(i * 131 + 7));
+        gguf.resize(data_offset + pos, 0);
         for (int i = 0; i < 4; ++i)
             std::memcpy(gguf.data() + data_offset + table[i].source_offset, hs[i]->data(), hs[i]->size());
+        const std::string gfile = "/tmp/ffn_path_test_" + std::to_string(getpid()) + ".gguf";
+        {
+            FILE *fo = std::fopen(gfile.c_str(), "wb");
+            expect(fo && std::fwrite(gguf.data(), 1, gguf.size(), fo) == gguf.size(), "GGUF file written");
+            if (fo) std::fclose(fo);
+        }
+        GGUF gg(gfile, false);
+        expect(gg.data_offset() == data_offset && gg.file_size() == gguf.size() && gg.meta_u64("general.alignment") == 65536,
+               "GGUF: data offset, size and alignment");
+        expect(gg.tensor("blk.0.ffn_down.weight").bytes == down.bytes && gg.has_tensor("token_embd.weight") &&
+                   !gg.has_tensor("blk.0.attn_q.weight"),
+               "GGUF: tensor lookup");
+        const std::vector<ns_tensor_desc> gt = gg.ffn_tensor_table();
+        bool same = gt.size() == table.size();
+        for (size_t i = 0; same && i < gt.size(); ++i)
+            same = gt[i].source_offset == table[i].source_offset && gt[i].bytes == table[i].bytes &&
+                   gt[i].type == table[i].type && gt[i].layer == table[i].layer && gt[i].kind == table[i].kind;
+        expect(same, "GGUF: the FFN tensor table from the file equals the engine's");
+        threw = false;
+        try { (void)gg.tensor("blk.0.attn_q.weight"); } catch (const std::runtime_error &e) { threw = std::strstr(e.what(), "missing tensor") != nullptr; }
+        expect(threw, "GGUF: missing tensor throws the reference's message");
+        std::remove(gfile.c_str());
         const std::string file = "/tmp/ffn_path_test_" + std::to_string(getpid()) + ".nsmffn";
-        convert_metal_ffn(file, gguf.data(), gguf.size(), data_offset, table);
+        convert_metal_ffn(file, gguf.data(), gguf.size(), data_offset, gt);
         const uint64_t fp = metal_ffn_fingerprint(gguf.data(), data_offset, gguf.size());
         MetalFfnFile mf(file, gguf.size(), fp, table);
         expect(mf.reordered(table[0].source_offset) && !mf.reordered(table[3].source_offset),
