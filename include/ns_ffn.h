@@ -76,7 +76,9 @@ int ns_ctx_destroy(ns_ctx *ctx);
  *   batch == 1, fp32 input      -> dequant-fused GEMV (decode; lm-head with ROW_MAJOR or CDNA4).
  *   batch 2-4, fp32 or fp16     -> small-batch GEMV streaming the weights once for all tokens
  *                                  (gemma_q4k/q6k_mm_fast[_f16][_metal], metal:125-177, mm:273).
- *   batch  > 4, half_input != 0 -> dequant-into-LDS MFMA GEMM, FP32 accumulation.
+ *   batch  > 4, half_input != 0 -> dequant-into-LDS MFMA GEMM, FP32 accumulation (any layout:
+ *                                  the reference's swizzled row-major kernels, metal:263-301,
+ *                                  432-478, serve attention tensors that stay row-major).
  *   batch  > 4, fp32 input      -> one GEMV per token.
  * `in` is fp32 [batch][cols] or, with half_input, fp16 bits [batch][cols]; out fp32 [batch][rows]. */
 int ns_matmul(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, uint32_t rows,
@@ -138,6 +140,23 @@ int ns_rmsnorm_add_then(ns_ctx *ctx, const float *x, const float *weight, const 
 int ns_rms_gate_up_geglu_decode(ns_ctx *ctx, const void *wg, const void *wu, int layout, uint32_t cols,
                                 uint32_t rows, const float *x, const float *norm_weight, float eps, float *h,
                                 void *stream);
+
+/* gemma_q6k_embedding (metal:503-505; the token embedding at mm:310, scale = sqrt(3840)):
+ * out[t][i] = scale * W[ids[t]][i], fp32 [batch][cols], each value as quant.cpp computes it.
+ * Q4_K or Q6_K in any layout (the engine may re-tile the embedding for the lm-head GEMV).  An id
+ * outside [0, rows) yields a row of NaN (the reference does not check). */
+int ns_embedding(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, uint32_t rows,
+                 const int32_t *ids, uint32_t batch, float scale, float *out, void *stream);
+
+/* qkv (mm:311; gemma_qkv_q4_f16 / _q6v_f16 / _tied_v_f16, metal:442-454): the attention
+ * projections of one layer in prefill.  x fp16 bits [batch][cols]; q fp32 [batch][q_rows];
+ * k, v fp32 [batch][kv_rows].  wq, wk Q4_K; wv of v_type (Q4_K or Q6_K), or NULL for tied V
+ * (V = K).  FP32 accumulation.  batch >= 2 (batch 2-4: the small-batch kernels; larger: the
+ * prefill GEMM); any layout, ROW_MAJOR being the reference's (attention weights are not
+ * re-laid by .nsmffn). */
+int ns_qkv(ns_ctx *ctx, const void *wq, const void *wk, const void *wv, int v_type, int layout, uint32_t cols,
+           uint32_t q_rows, uint32_t kv_rows, uint32_t batch, const uint16_t *x, float *q, float *k, float *v,
+           void *stream);
 
 /* ---- host-side (CPU) utilities; no GPU needed ------------------------------ */
 

@@ -92,8 +92,6 @@ int gemv_mt(ns_ctx *ctx, const char *fn, int type, int layout, const void *w, co
 
 int gemm(ns_ctx *ctx, const char *fn, int type, int layout, int acc, const void *w, const void *up,
          const uint16_t *x, void *out, uint32_t cols, uint32_t rows, uint32_t batch, hipStream_t s) {
-    if (layout == ROW_MAJOR)
-        return fail(NS_ERR_UNSUPPORTED, std::string(fn) + ": the prefill GEMM needs the NSMFFN or CDNA4 slab layout");
     size_t wf = 0, wc = 0;
     gemm_workspace_need(type, layout, cols, rows, batch, up != nullptr, &wf, &wc);
     if (int rc = ensure_ws(ctx, wf, wc)) return rc;
@@ -278,4 +276,40 @@ extern "C" int ns_rms_gate_up_geglu_decode(ns_ctx *ctx, const void *wg, const vo
     np.wb = norm_weight;
     np.eps = eps;
     return rms_gate_up(ctx, "ns_rms_gate_up_geglu_decode", wg, wu, layout, cols, rows, np, h, stream);
+}
+
+extern "C" int ns_embedding(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, uint32_t rows,
+                            const int32_t *ids, uint32_t batch, float scale, float *out, void *stream) {
+    if (!ctx) return fail(NS_ERR_ARG, "ns_embedding: null context");
+    if (int rc = check_tensor("ns_embedding", w, type, layout, cols, rows)) return rc;
+    if (!ids || !out || batch == 0) return fail(NS_ERR_ARG, "ns_embedding: null ids/output or zero batch");
+    const hipError_t e = launch_embedding(type, layout, static_cast<const uint8_t *>(w), cols, rows, ids, batch, scale,
+                                          out, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? NS_OK : hip_fail(e, "ns_embedding");
+}
+
+extern "C" int ns_qkv(ns_ctx *ctx, const void *wq, const void *wk, const void *wv, int v_type, int layout,
+                      uint32_t cols, uint32_t q_rows, uint32_t kv_rows, uint32_t batch, const uint16_t *x, float *q,
+                      float *k, float *v, void *stream) {
+    const char *fn = "ns_qkv";
+    if (!ctx) return fail(NS_ERR_ARG, "ns_qkv: null context");
+    if (int rc = check_tensor(fn, wq, Q4_K, layout, cols, q_rows)) return rc;
+    if (int rc = check_tensor(fn, wk, Q4_K, layout, cols, kv_rows)) return rc;
+    if (wv)
+        if (int rc = check_tensor(fn, wv, v_type, layout, cols, kv_rows)) return rc;
+    if (!x || !q || !k || !v) return fail(NS_ERR_ARG, "ns_qkv: null input/output");
+    if (batch < 2) return fail(NS_ERR_UNSUPPORTED, "ns_qkv: the fused projection is the prefill path (batch >= 2)");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    // Q, K and V each stream their own weights once; x (fp16 [batch][cols]) is re-read
+    // from the caches.  Batch 2-4 takes the small-batch kernels, larger batches the GEMM.
+    auto proj = [&](const void *w, int type, uint32_t rows, float *out) {
+        if (batch <= 4) return gemv_mt(ctx, fn, type, layout, w, nullptr, x, true, batch, out, cols, rows, s);
+        return gemm(ctx, fn, type, layout, ACC_FP32, w, nullptr, x, out, cols, rows, batch, s);
+    };
+    if (int rc = proj(wq, Q4_K, q_rows, q)) return rc;
+    if (int rc = proj(wk, Q4_K, kv_rows, k)) return rc;
+    if (wv) return proj(wv, v_type, kv_rows, v);
+    // tied V (gemma_qkv_tied_v_f16, metal:454): V is K
+    const hipError_t e = hipMemcpyAsync(v, k, size_t(batch) * kv_rows * sizeof(float), hipMemcpyDeviceToDevice, s);
+    return e == hipSuccess ? NS_OK : hip_fail(e, fn);
 }

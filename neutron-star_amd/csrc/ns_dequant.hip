@@ -23,16 +23,9 @@ __device__ __forceinline__ uint32_t rd32(const uint8_t *w, int type, int layout,
     return rd16(w, type, layout, row, kb, nb, j) | (rd16(w, type, layout, row, kb, nb, j + 2) << 16);
 }
 
-// One thread per (row, 32-element group of one super-block).
-__global__ void dequant_kernel(const uint8_t *__restrict__ w, int type, int layout, uint32_t cols,
-                               uint32_t row0, uint32_t nrows, float *__restrict__ out32,
-                               uint16_t *__restrict__ out16) {
-    const uint32_t groups = cols / 32;
-    const uint64_t idx = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (idx >= uint64_t(nrows) * groups) return;
-    const uint32_t rr = uint32_t(idx / groups), gi = uint32_t(idx % groups);
-    const uint32_t row = row0 + rr, nb = cols / kQK, kb = gi / 8, g = gi % 8;
-    float v[32];
+// The 32 values of group g (0..7) of super-block kb of `row`, as quant.cpp computes them.
+__device__ void group_values(const uint8_t *__restrict__ w, int type, int layout, uint32_t row, uint32_t kb,
+                             uint32_t nb, uint32_t g, float (&v)[32]) {
     if (type == Q4_K) {
         const uint32_t hdr = rd32(w, type, layout, row, kb, nb, 0);
         const Q4Scales s = q4_scales(rd32(w, type, layout, row, kb, nb, 4), rd32(w, type, layout, row, kb, nb, 8),
@@ -56,11 +49,43 @@ __global__ void dequant_kernel(const uint8_t *__restrict__ w, int type, int layo
             v[l] = q6_value(d * float(sc), vv & 0xffu);
         }
     }
+}
+
+// One thread per (row, 32-element group of one super-block).
+__global__ void dequant_kernel(const uint8_t *__restrict__ w, int type, int layout, uint32_t cols,
+                               uint32_t row0, uint32_t nrows, float *__restrict__ out32,
+                               uint16_t *__restrict__ out16) {
+    const uint32_t groups = cols / 32;
+    const uint64_t idx = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= uint64_t(nrows) * groups) return;
+    const uint32_t rr = uint32_t(idx / groups), gi = uint32_t(idx % groups);
+    float v[32];
+    group_values(w, type, layout, row0 + rr, gi / 8, cols / kQK, gi % 8, v);
     const size_t o = size_t(rr) * cols + size_t(gi) * 32;
     for (int l = 0; l < 32; ++l) {
         if (out32) out32[o + l] = v[l];
         if (out16) out16[o + l] = __builtin_bit_cast(uint16_t, _Float16(v[l]));
     }
+}
+
+// Embedding lookup (gemma_q6k_embedding, metal:503-505): out[t][i] = scale * value(ids[t], i),
+// one thread per (token, 32-element group).  An id outside [0, rows) writes NaN.
+__global__ void embedding_kernel(const uint8_t *__restrict__ w, int type, int layout, uint32_t cols, uint32_t rows,
+                                 const int32_t *__restrict__ ids, uint32_t batch, float scale,
+                                 float *__restrict__ out) {
+    const uint32_t groups = cols / 32;
+    const uint64_t idx = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= uint64_t(batch) * groups) return;
+    const uint32_t t = uint32_t(idx / groups), gi = uint32_t(idx % groups);
+    const int32_t id = ids[t];
+    float *o = out + size_t(t) * cols + size_t(gi) * 32;
+    if (id < 0 || uint32_t(id) >= rows) {
+        for (int l = 0; l < 32; ++l) o[l] = __builtin_nanf("");
+        return;
+    }
+    float v[32];
+    group_values(w, type, layout, uint32_t(id), gi / 8, cols / kQK, gi % 8, v);
+    for (int l = 0; l < 32; ++l) o[l] = scale * v[l];
 }
 
 // One thread per (row, super-block): moves the block's 2-byte units.
@@ -85,6 +110,15 @@ hipError_t launch_dequant(int type, int layout, const uint8_t *w, uint32_t cols,
     if (!n) return hipSuccess;
     dequant_kernel<<<dim3(uint32_t((n + 255) / 256)), dim3(256), 0, stream>>>(w, type, layout, cols, row0, nrows,
                                                                               out_f32, out_f16);
+    return hipGetLastError();
+}
+
+hipError_t launch_embedding(int type, int layout, const uint8_t *w, uint32_t cols, uint32_t rows, const int32_t *ids,
+                            uint32_t batch, float scale, float *out, hipStream_t stream) {
+    const uint64_t n = uint64_t(batch) * (cols / 32);
+    if (!n) return hipSuccess;
+    embedding_kernel<<<dim3(uint32_t((n + 255) / 256)), dim3(256), 0, stream>>>(w, type, layout, cols, rows, ids, batch,
+                                                                                scale, out);
     return hipGetLastError();
 }
 

@@ -128,7 +128,7 @@ __device__ __forceinline__ void load_raw(rsrc_t w, uint32_t row, uint32_t nb, ui
         r.hdr = bload16(w, base);
         r.qs = bload16(w, base + (1 + 2 * p + hh) * kRowTile * 16);
     } else {
-        const uint32_t blk = uint32_t(block_index(NSMFFN, row, b, nb)) * kQ4Bytes;
+        const uint32_t blk = uint32_t(block_index(LAYOUT, row, b, nb)) * kQ4Bytes;
         r.hdr = bload16(w, blk);
         r.qs = bload16(w, blk + (1 + 2 * p + hh) * 16);
     }
@@ -185,7 +185,7 @@ __device__ __forceinline__ void load_raw(rsrc_t w, uint32_t row, uint32_t nb, ui
         r.scw = bload16(w, base + 12 * kRowTile * 16);
         r.dbits = bload2(w, reg + kQ6Chunks * 1024 + (row % kRowTile) * 2);
     } else {
-        const uint32_t blk = uint32_t(block_index(NSMFFN, row, b, nb)) * kQ6Bytes;
+        const uint32_t blk = uint32_t(block_index(LAYOUT, row, b, nb)) * kQ6Bytes;
         r.ql[0] = load_chunk_q6(w, blk, cl);
         r.ql[1] = load_chunk_q6(w, blk, cl + 1);
         r.qh[0] = load_chunk_q6(w, blk, chh);
@@ -657,7 +657,9 @@ hipError_t launch_layout(int layout, int acc, const uint8_t *w, const uint8_t *u
                          const Workspace &ws, size_t ws_offset, hipStream_t stream) {
     if (layout == CDNA4)
         return launch_mode<TYPE, CDNA4, PAIR>(acc, w, up, x, xh, out, cols, rows, batch, ws, ws_offset, stream);
-    return launch_mode<TYPE, NSMFFN, PAIR>(acc, w, up, x, xh, out, cols, rows, batch, ws, ws_offset, stream);
+    if (layout == NSMFFN)
+        return launch_mode<TYPE, NSMFFN, PAIR>(acc, w, up, x, xh, out, cols, rows, batch, ws, ws_offset, stream);
+    return launch_mode<TYPE, ROW_MAJOR, PAIR>(acc, w, up, x, xh, out, cols, rows, batch, ws, ws_offset, stream);
 }
 
 }  // namespace

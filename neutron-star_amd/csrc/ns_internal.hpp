@@ -84,6 +84,10 @@ hipError_t launch_rmsnorm(const float *x, const float *w, const float *residual,
                           const float *next_w, uint32_t rows, uint32_t width, float eps, void *y, bool half_y,
                           void *next, bool half_next, hipStream_t stream);
 
+// out[t][i] = scale * W[ids[t]][i] (fp32 values as quant.cpp; NaN rows for ids out of range).
+hipError_t launch_embedding(int type, int layout, const uint8_t *w, uint32_t cols, uint32_t rows, const int32_t *ids,
+                            uint32_t batch, float scale, float *out, hipStream_t stream);
+
 hipError_t launch_retile(int type, const uint8_t *src, uint8_t *dst, uint32_t cols,
                          uint32_t rows, int from_layout, int to_layout, hipStream_t stream);
 

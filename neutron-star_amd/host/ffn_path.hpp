@@ -166,6 +166,23 @@ public:
         ffn_down(e, down, mid, out, batch, prefill, fast_swa);
     }
 
+    // qkv (mm:311): Q, K and V projections of fp16 `in` ([batch][cols]) into fp32 q, k, v;
+    // wv == nullptr is the tied-V model (V = K).  batch >= 2.
+    void qkv(hipStream_t e, const Tensor &wq, const Tensor &wk, const Tensor *wv, const uint16_t *in, float *q,
+             float *k, float *v, uint32_t batch) const {
+        if (wq.shape.at(0) != wk.shape.at(0) || w_.layout(wq) != w_.layout(wk) ||
+            (wv && (wv->shape != wk.shape || w_.layout(*wv) != w_.layout(wk))))
+            throw std::runtime_error("qkv tensors differ in input width, kv shape or layout: " + wq.name);
+        check(ns_qkv(ctx_, w_.data(wq), w_.data(wk), wv ? w_.data(*wv) : nullptr, wv ? int(wv->type) : int(wk.type),
+                     int(w_.layout(wq)), cols(wq), rows(wq), rows(wk), batch, in, q, k, v, e));
+    }
+    // The token embedding (mm:310, gemma_q6k_embedding): out[t] = scale * embedding[ids[t]].
+    void embedding(hipStream_t e, const Tensor &emb, const int32_t *ids, uint32_t batch, float scale,
+                   float *out) const {
+        check(ns_embedding(ctx_, w_.data(emb), int(emb.type), int(w_.layout(emb)), cols(emb), rows(emb), ids, batch,
+                           scale, out, e));
+    }
+
     // The RMSNorm helpers around the FFN block (mm:291-296; metal:509-529).  Norm
     // weights are fp32 device vectors of `width`; eps is the model's epsilon.
     // rms (mm:291): out = (in * r) * w per row, r = 1/sqrt(mean(in^2) + eps).

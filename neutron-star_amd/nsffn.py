@@ -83,6 +83,8 @@ def lib():
             "ns_nsmffn_open": [ctypes.c_char_p, u64, u64, vp, u32, ctypes.POINTER(vp)],
             "ns_nsmffn_close": [vp],
             "ns_nsmffn_lookup": [vp, u64, ctypes.POINTER(u64), ctypes.POINTER(i32)],
+            "ns_embedding": [vp, vp, i32, i32, u32, u32, vp, u32, ctypes.c_float, vp, vp],
+            "ns_qkv": [vp, vp, vp, vp, i32, i32, u32, u32, u32, u32, vp, vp, vp, vp, vp],
             "ns_gguf_open": [ctypes.c_char_p, i32, ctypes.POINTER(vp)],
             "ns_gguf_close": [vp],
             "ns_gguf_tensor": [vp, u32, ctypes.POINTER(GgufTensorInfo)],
@@ -391,6 +393,16 @@ class Context:
         """rms (mm:563) then gate_up_geglu_decode (mm:571), one launch."""
         check(lib().ns_rms_gate_up_geglu_decode(self.handle, _ptr(wg), _ptr(wu), layout, cols, rows, _ptr(x),
                                                 _ptr(norm_weight), eps, _ptr(h), _stream(stream)))
+
+    def embedding(self, w, qtype, layout, cols, rows, ids, batch, scale, out, stream=None):
+        """gemma_q6k_embedding (metal:503): out[t] = scale * W[ids[t]]."""
+        check(lib().ns_embedding(self.handle, _ptr(w), qtype, layout, cols, rows, _ptr(ids), batch, scale, _ptr(out),
+                                 _stream(stream)))
+
+    def qkv(self, wq, wk, wv, v_type, layout, cols, q_rows, kv_rows, batch, x, q, k, v, stream=None):
+        """qkv (mm:311): Q, K, V projections of fp16 x; wv None for tied V."""
+        check(lib().ns_qkv(self.handle, _ptr(wq), _ptr(wk), _ptr(wv), v_type, layout, cols, q_rows, kv_rows, batch,
+                           _ptr(x), _ptr(q), _ptr(k), _ptr(v), _stream(stream)))
 
     def dequant(self, w, qtype, layout, cols, rows, row0, nrows, out_f32=None, out_f16=None, stream=None):
         check(lib().ns_dequant(self.handle, _ptr(w), qtype, layout, cols, rows, row0, nrows,
