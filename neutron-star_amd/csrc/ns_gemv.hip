@@ -34,12 +34,14 @@ namespace {
 
 constexpr uint32_t kWgWaves = 4;   // waves per workgroup of the flattened split
 
-// Largest workgroup (in waves) a kernel instance supports: as many as one CU
-// holds at that kernel's register use.  With the prefetch buffer (PF): Q4_K
-// ~110 VGPRs, 4 waves per SIMD; Q6_K ~150: 3; gate/up pair ~190: 2.  Without
-// it every instance fits in 128 VGPRs, 4 waves per SIMD.
+// Largest workgroup (in waves) a kernel instance supports.  Without the
+// prefetch buffer every instance fits in 128 VGPRs, 4 waves per SIMD.  The
+// streaming (PF) Q4_K and Q6_K instances hold two unit buffers in up to 256
+// VGPRs (two waves per SIMD) and run 4-wave workgroups; the PF gate/up pair
+// (~190 VGPRs) fits 2 waves per SIMD.
 constexpr uint32_t max_wg_waves(int type, bool pair, bool pf) {
-    return !pf ? 16 : pair ? 8 : (type == Q4_K ? 16 : 12);
+    (void)type;
+    return !pf ? 16 : pair ? 8 : 4;
 }
 
 // ---- block loads --------------------------------------------------------
@@ -340,8 +342,7 @@ __device__ __forceinline__ void group_sums_x(const void *__restrict__ xb, uint32
 // values), returned wave-uniform.  Each lane adds 4 values; the groups are
 // completed with cross-lane exchanges and read back with readlane.
 template <int GROUP>
-__device__ __forceinline__ void group_sums(const float *__restrict__ xb, uint32_t lane, float *xs) {
-    const float4 v = reinterpret_cast<const float4 *>(xb)[lane];
+__device__ __forceinline__ void group_sums_of(const float4 &v, float *xs) {
     float s = (v.x + v.y) + (v.z + v.w);
     s += __shfl_xor(s, 1);
     s += __shfl_xor(s, 2);
@@ -349,6 +350,20 @@ __device__ __forceinline__ void group_sums(const float *__restrict__ xb, uint32_
 #pragma unroll
     for (int g = 0; g < 256 / GROUP; ++g)
         xs[g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), g * (GROUP / 4)));
+}
+
+template <int GROUP>
+__device__ __forceinline__ void group_sums(const float *__restrict__ xb, uint32_t lane, float *xs) {
+    group_sums_of<GROUP>(reinterpret_cast<const float4 *>(xb)[lane], xs);
+}
+
+// A streaming loop loads the lane's float4 of x for the group sums together with
+// the unit's weights.  Vector memory operations complete in order, so a load of x
+// issued after the next unit's prefetch would make the current unit wait for
+// the whole prefetch.  (The dot products read x with scalar loads, which are
+// counted apart from vector memory operations.)
+__device__ __forceinline__ float4 x_lane(const float *__restrict__ x, uint32_t b, uint32_t lane) {
+    return reinterpret_cast<const float4 *>(x + size_t(b) * kQK)[lane];
 }
 
 // Flattened work: unit i = (slab i / nb, super-block i % nb), i < U = nslabs * nb.
@@ -418,7 +433,7 @@ __device__ void norm_finish(RmsRow<1> &rr, const NormPrologue &np, uint32_t cols
 //      A workgroup barrier at the start would hold every wave until the last
 //      one of its workgroup had been dispatched and had its row.
 template <int TYPE, int LAYOUT, bool PAIR, bool PF, int XL>
-__global__ __launch_bounds__(max_wg_waves(TYPE, PAIR, PF) * 64) void gemv_kernel(
+__global__ __launch_bounds__(max_wg_waves(TYPE, PAIR, PF) * 64, PF && !PAIR ? 2 : 1) void gemv_kernel(
     const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, const float *__restrict__ xg,
     float *__restrict__ out, uint32_t rows, uint32_t nb, uint32_t nslabs, float *__restrict__ partial,
     uint32_t *__restrict__ counters, const NormPrologue np) {
@@ -501,18 +516,93 @@ __global__ __launch_bounds__(max_wg_waves(TYPE, PAIR, PF) * 64) void gemv_kernel
 
     // Each branch requests the first unit's weights, runs the prologue (all
     // threads of the workgroup: it has barriers), then walks the wave's units.
-    if constexpr (TYPE == Q4_K) {
+    if constexpr (PF && XL == 0 && !PAIR) {
+        // The streaming loop.  Two unit buffers alternate (A, B), so a prefetch
+        // lands in the registers its compute reads (a loop-carried buffer is
+        // copied at the end of each iteration, and the copy waits for the
+        // prefetch), and no load is issued under a condition that later merges:
+        // each compute then waits for its own unit's loads only.  x's float4 for
+        // the group sums travels with the weights (vector memory operations
+        // complete in order; a load of x issued after the prefetch would make
+        // the compute wait for the whole prefetch).  (The gate/up pair keeps the
+        // loop below: two pair buffers do not fit 256 VGPRs without spills.)
+        constexpr int N = PAIR ? 2 : 1;
+        struct Buf {
+            u32x4 c[N][TYPE == Q4_K ? kQ4Chunks : kQ6Chunks];
+            uint32_t d;
+            float4 xv;
+        };
+        auto load = [&](Buf &f, uint32_t s, uint32_t bb) {
+            if constexpr (TYPE == Q4_K) {
+                q4_load<LAYOUT>(w0, lane, lrow(s), s, bb, nb, f.c[0]);
+                if constexpr (PAIR) q4_load<LAYOUT>(w1, lane, lrow(s), s, bb, nb, f.c[N - 1]);
+            } else {
+                q6_load<LAYOUT>(w0, lane, lrow(s), s, bb, nb, f.c[0], f.d);
+            }
+            f.xv = x_lane(x, bb, lane);
+        };
+        // unit i (at slab, b) from buffer f
+        auto unit = [&](const Buf &f, uint32_t i) {
+            const float *xb = x + size_t(b) * kQK;
+            if constexpr (TYPE == Q4_K) {
+                float xs[8], r[N];
+                group_sums_of<32>(f.xv, xs);
+                q4_dot<N>(f.c, xb, xs, r);
+                acc0 += r[0];
+                if constexpr (PAIR) acc1 += r[N - 1];
+            } else {
+                float xs[16];
+                group_sums_of<16>(f.xv, xs);
+                acc0 += q6_dot(f.c[0], f.d, xb, xs);
+            }
+            step_done(i);
+        };
+        if (i0 < i1) {
+            Buf A, B;
+            load(A, slab, b);
+            uint32_t i = i0;
+            while (true) {
+                if (i + 1 == i1) {
+                    unit(A, i);
+                    break;
+                }
+                uint32_t ns_ = slab, nbk = b;
+                advance(ns_, nbk);
+                load(B, ns_, nbk);
+                __builtin_amdgcn_sched_barrier(0);
+                unit(A, i);
+                slab = ns_;
+                b = nbk;
+                if (++i + 1 == i1) {
+                    unit(B, i);
+                    break;
+                }
+                ns_ = slab;
+                nbk = b;
+                advance(ns_, nbk);
+                load(A, ns_, nbk);
+                __builtin_amdgcn_sched_barrier(0);
+                unit(B, i);
+                slab = ns_;
+                b = nbk;
+                ++i;
+            }
+        }
+    } else if constexpr (TYPE == Q4_K) {
         constexpr int N = PAIR ? 2 : 1;
         const uint8_t *wm[2] = {w0, w1};
-        auto compute = [&](const u32x4(&cc)[N][kQ4Chunks]) {
+        // xv: the lane's float4 of x, loaded with the weights (PF from global memory)
+        auto compute = [&](const u32x4(&cc)[N][kQ4Chunks], const float4 &xv) {
             const float *xb = x + size_t(b) * kQK;
             float xs[8], r[N];
-            group_sums<32>(xb, lane, xs);
+            if constexpr (PF && !XL) group_sums_of<32>(xv, xs);
+            else group_sums<32>(xb, lane, xs);
             q4_dot<N>(cc, xb, xs, r);
             acc0 += r[0];
             if constexpr (PAIR) acc1 += r[N - 1];
         };
         u32x4 c[N][kQ4Chunks];
+        float4 xc{};
         if constexpr (XL) {
             // Unconditional (a wave without units loads the last unit and drops it), so
             // the wait for the prologue's row counts these loads as still outstanding.
@@ -520,9 +610,11 @@ __global__ __launch_bounds__(max_wg_waves(TYPE, PAIR, PF) * 64) void gemv_kernel
 #pragma unroll
             for (int m = 0; m < N; ++m) q4_load<LAYOUT>(wm[m], lane, lrow(su), su, bu, nb, c[m]);
         } else if constexpr (PF) {
-            if (i0 < i1)
+            if (i0 < i1) {
 #pragma unroll
                 for (int m = 0; m < N; ++m) q4_load<LAYOUT>(wm[m], lane, lrow(slab), slab, b, nb, c[m]);
+                xc = x_lane(x, b, lane);
+            }
         }
         prologue();
         if constexpr (PF) {
@@ -530,10 +622,13 @@ __global__ __launch_bounds__(max_wg_waves(TYPE, PAIR, PF) * 64) void gemv_kernel
                 uint32_t ns_ = slab, nbk = b;
                 advance(ns_, nbk);
                 u32x4 nx[N][kQ4Chunks];
-                if (i + 1 < i1)
+                float4 xn{};
+                if (i + 1 < i1) {
 #pragma unroll
                     for (int m = 0; m < N; ++m) q4_load<LAYOUT>(wm[m], lane, lrow(ns_), ns_, nbk, nb, nx[m]);
-                compute(c);
+                    if constexpr (!XL) xn = x_lane(x, nbk, lane);
+                }
+                compute(c, xc);
                 step_done(i);
                 slab = ns_;
                 b = nbk;
@@ -541,30 +636,36 @@ __global__ __launch_bounds__(max_wg_waves(TYPE, PAIR, PF) * 64) void gemv_kernel
                 for (int m = 0; m < N; ++m)
 #pragma unroll
                     for (int k = 0; k < int(kQ4Chunks); ++k) c[m][k] = nx[m][k];
+                xc = xn;
             }
         } else if constexpr (XL == 2) {
-            compute(c);  // exactly one unit per wave (W = nb, one slab per workgroup)
+            compute(c, xc);  // exactly one unit per wave (W = nb, one slab per workgroup)
             step_done(i0);
         } else {
             for (uint32_t i = i0; i < i1; ++i) {
                 if (!XL || i != i0)
 #pragma unroll
                     for (int m = 0; m < N; ++m) q4_load<LAYOUT>(wm[m], lane, lrow(slab), slab, b, nb, c[m]);
-                compute(c);
+                compute(c, xc);
                 step_done(i);
                 advance(slab, b);
             }
         }
     } else {
-        auto compute = [&](const u32x4(&cc)[kQ6Chunks], uint32_t dd) {
+        auto compute = [&](const u32x4(&cc)[kQ6Chunks], uint32_t dd, const float4 &xv) {
             const float *xb = x + size_t(b) * kQK;
             float xs[16];
-            group_sums<16>(xb, lane, xs);
+            if constexpr (PF && !XL) group_sums_of<16>(xv, xs);
+            else group_sums<16>(xb, lane, xs);
             acc0 += q6_dot(cc, dd, xb, xs);
         };
         u32x4 c0[kQ6Chunks];
         uint32_t d0 = 0;
-        if ((PF || XL) && i0 < i1) q6_load<LAYOUT>(w0, lane, lrow(slab), slab, b, nb, c0, d0);
+        float4 xc{};
+        if ((PF || XL) && i0 < i1) {
+            q6_load<LAYOUT>(w0, lane, lrow(slab), slab, b, nb, c0, d0);
+            if constexpr (PF && !XL) xc = x_lane(x, b, lane);
+        }
         prologue();
         if constexpr (PF) {
             for (uint32_t i = i0; i < i1; ++i) {
@@ -572,19 +673,24 @@ __global__ __launch_bounds__(max_wg_waves(TYPE, PAIR, PF) * 64) void gemv_kernel
                 advance(ns_, nbk);
                 u32x4 n0[kQ6Chunks];
                 uint32_t dn = 0;
-                if (i + 1 < i1) q6_load<LAYOUT>(w0, lane, lrow(ns_), ns_, nbk, nb, n0, dn);
-                compute(c0, d0);
+                float4 xn{};
+                if (i + 1 < i1) {
+                    q6_load<LAYOUT>(w0, lane, lrow(ns_), ns_, nbk, nb, n0, dn);
+                    if constexpr (!XL) xn = x_lane(x, nbk, lane);
+                }
+                compute(c0, d0, xc);
                 step_done(i);
                 slab = ns_;
                 b = nbk;
 #pragma unroll
                 for (int k = 0; k < int(kQ6Chunks); ++k) c0[k] = n0[k];
                 d0 = dn;
+                xc = xn;
             }
         } else {
             for (uint32_t i = i0; i < i1; ++i) {
                 if (!XL || i != i0) q6_load<LAYOUT>(w0, lane, lrow(slab), slab, b, nb, c0, d0);
-                compute(c0, d0);
+                compute(c0, d0, xc);
                 step_done(i);
                 advance(slab, b);
             }
@@ -918,16 +1024,29 @@ struct GemvPlan {
 };
 
 // G: as many workgroups as the device holds at once (never more than there
-// are units).  Measured on MI355X this is at or near the best grid for every
-// shape of the path: the 262144-row lm-head (4096 slabs, 1.3 slabs per wave),
-// the 3840-row down projection and the 15360-row gate/up projections.
-GemvPlan plan_gemv(uint32_t cols, uint32_t rows, int resident_waves, uint32_t max_waves, uint32_t cus) {
+// are units).  With slab_per_wg (the batch-1 streaming Q4_K/Q6_K instance) and
+// at least two slabs per resident workgroup, one workgroup per slab instead:
+// its 4 waves split the slab's super-blocks and meet in LDS, nothing crosses
+// workgroups, and the dispatcher gives a CU its next slab as one finishes, so
+// CUs that stream faster take more slabs.  Measured on MI355X, 262,144-row
+// lm-head (4096 slabs, 2048 resident waves): one slab per workgroup 122.9 us;
+// one slab per wave (4096 waves) 125.1 us; the resident grid (two slabs per
+// wave) 127.2 us; 12288 waves (slabs cut between workgroups) 130.6 us.
+// NS_GEMV_WAVES sets the flattened grid's wave count instead.
+GemvPlan plan_gemv(uint32_t cols, uint32_t rows, int resident_waves, uint32_t max_waves, uint32_t cus,
+                   bool slab_per_wg) {
     GemvPlan p;
     const uint32_t nb = cols / kQK;
     p.nslabs = (rows + kRowTile - 1) / kRowTile;
     const uint32_t U = p.nslabs * nb;
     uint32_t cap = uint32_t(resident_waves > 0 ? resident_waves : 2048);
-    if (const int e = env_int("NS_GEMV_WAVES", 0); e > 0) cap = uint32_t(e);
+    const int forced = env_int("NS_GEMV_WAVES", 0);
+    if (forced > 0) cap = uint32_t(forced);
+    if (slab_per_wg && forced <= 0 && p.nslabs >= 2 * ((cap + kWgWaves - 1) / kWgWaves)) {
+        p.W = kWgWaves < nb ? kWgWaves : nb;
+        p.G = p.nslabs;
+        return p;
+    }
     // About one slab per CU (the 15360-row gate/up projections: 240 slabs): one
     // workgroup per slab, as many waves as the CU holds -- nothing crosses
     // workgroups.  Otherwise the flattened split over resident 4-wave workgroups.
@@ -987,7 +1106,8 @@ GemvChoice choose_gemv(int layout, uint32_t cols, uint32_t rows) {
     const int force = env_int("NS_GEMV_PF", -1);
     const bool one = force == 0 || (force < 0 && int(units) <= resident_waves<TYPE, PAIR, false>(layout));
     if (one) return {plan_one_unit(cols, rows, cus, uint32_t(resident_waves<TYPE, PAIR, false>(layout)) / cus), false};
-    return {plan_gemv(cols, rows, resident_waves<TYPE, PAIR, true>(layout), max_wg_waves(TYPE, PAIR, true), cus),
+    return {plan_gemv(cols, rows, resident_waves<TYPE, PAIR, true>(layout), max_wg_waves(TYPE, PAIR, true), cus,
+                      !PAIR),
             true};
 }
 
@@ -1056,7 +1176,7 @@ struct Mt {
             w = wgs * kWgWaves;
         }
         const uint32_t cus = uint32_t(device_shape().cus);
-        return plan_gemv(cols, rows, w * int(cus), max_wg_waves_mt(TYPE, PAIR, NT), cus);
+        return plan_gemv(cols, rows, w * int(cus), max_wg_waves_mt(TYPE, PAIR, NT), cus, false);
     }
 };
 

@@ -104,6 +104,83 @@ def test_lm_head_gemv(ctx, layout):
     assert rel_err(y.cpu().numpy(), ref) <= TOL32
 
 
+# ---- the streaming GEMV (the lm-head instance) ----------------------------------
+# With at least two slabs per resident workgroup the streaming instance gives
+# every slab its own 4-wave workgroup (parts meet in LDS); NS_GEMV_WAVES forces
+# the flattened grid instead (slabs cut between waves and workgroups).  Both
+# grids must meet the bar, and each must repeat bit for bit.
+
+def _lm_head(ctx, layout, rows=262144):
+    cols = 3840
+    host, w = weights(N.Q6_K, 9, rows, cols, layout)
+    x = f32(cols, 10)
+    return host, w, x, cols, rows
+
+
+def _run(ctx, qtype, w, layout, cols, rows, x):
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    ctx.matmul(w, qtype, layout, cols, rows, 1, torch.from_numpy(x).cuda(), y)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+@pytest.mark.parametrize("waves", [None, "2048", "12288"], ids=["slab_per_wg", "resident", "cut_slabs"])
+def test_stream_grids(ctx, monkeypatch, waves):
+    if waves:
+        monkeypatch.setenv("NS_GEMV_WAVES", waves)
+    host, w, x, cols, rows = _lm_head(ctx, N.CDNA4)
+    ref = O.gemv(N.Q6_K, O.ROW_MAJOR, host, cols, rows, x)
+    y = _run(ctx, N.Q6_K, w, N.CDNA4, cols, rows, x)
+    assert rel_err(y, ref) <= TOL32
+    assert np.array_equal(_run(ctx, N.Q6_K, w, N.CDNA4, cols, rows, x).view(np.uint32), y.view(np.uint32))
+
+
+def test_stream_repeated_launches(ctx):
+    """Back-to-back launches on one stream give identical results (the hand-off
+    counters of cut slabs return to zero after each launch)."""
+    _, w, x, cols, rows = _lm_head(ctx, N.CDNA4)
+    xd = torch.from_numpy(x).cuda()
+    ys = [torch.full((rows,), float("nan"), dtype=torch.float32, device="cuda") for _ in range(4)]
+    for y in ys:
+        ctx.matmul(w, N.Q6_K, N.CDNA4, cols, rows, 1, xd, y)
+    torch.cuda.synchronize()
+    assert not torch.isnan(ys[0]).any()
+    assert all(torch.equal(ys[0], t) for t in ys[1:])
+
+
+STREAM_CASES = [
+    (N.Q6_K, 3840, 262144 - 37, N.ROW_MAJOR, "lm_head_ragged"),
+    (N.Q4_K, 512, 192, N.CDNA4, "q4k_small"),
+    (N.Q6_K, 256, 64, N.NSMFFN, "q6k_one_slab"),
+    (N.Q4_K, 3840, 65536, N.NSMFFN, "q4k_wide"),
+    (N.Q6_K, 768, 131072, N.CDNA4, "q6k_three_blocks"),
+]
+
+
+@pytest.mark.parametrize("qtype,cols,rows,layout,name", STREAM_CASES, ids=[c[4] for c in STREAM_CASES])
+def test_stream_shapes(ctx, monkeypatch, qtype, cols, rows, layout, name):
+    """The streaming instance forced (NS_GEMV_PF=1) on shapes from one slab to a
+    ragged row-major lm-head, with fewer super-blocks per slab than waves."""
+    monkeypatch.setenv("NS_GEMV_PF", "1")
+    host, w = weights(qtype, 31, rows, cols, layout)
+    x = f32(cols, 32)
+    ref = O.gemv(qtype, O.ROW_MAJOR, host, cols, rows, x)
+    assert rel_err(_run(ctx, qtype, w, layout, cols, rows, x), ref) <= TOL32
+
+
+def test_stream_gate_up_pair(ctx, monkeypatch):
+    monkeypatch.setenv("NS_GEMV_PF", "1")
+    cols, rows = 3840, 15360
+    hg, wg = weights(N.Q4_K, 21, rows, cols, N.CDNA4)
+    hu, wu = weights(N.Q4_K, 22, rows, cols, N.CDNA4)
+    x = f32(cols, 23)
+    ref = O.gate_up_geglu(O.ROW_MAJOR, hg, hu, cols, rows, x)
+    h = torch.empty(rows, dtype=torch.float32, device="cuda")
+    ctx.gate_up_geglu_decode(wg, wu, N.CDNA4, cols, rows, torch.from_numpy(x).cuda(), h)
+    torch.cuda.synchronize()
+    assert rel_err(h.cpu().numpy(), ref) <= TOL32
+
+
 def test_gemv_deterministic(ctx):
     cols, rows = 15360, 3840
     _, w = weights(N.Q6_K, 11, rows, cols, N.CDNA4)
