@@ -734,11 +734,12 @@ __global__ __launch_bounds__(max_wg_waves(TYPE, PAIR, PF) * 64, PF && !PAIR ? 2 
             if (prev != gl - gf) continue;
             r0 = 0.f;
             r1 = 0.f;
-            // Parts of workgroups gf..gl, loaded 8 at a time and added in order.
-            for (uint32_t h0 = gf; h0 <= gl; h0 += 8) {
-                float v0[8], v1[8];
+            // Parts of workgroups gf..gl, loaded 16 at a time (one round trip for the
+            // 15 workgroups of a down-projection slab cut 15 ways) and added in order.
+            for (uint32_t h0 = gf; h0 <= gl; h0 += 16) {
+                float v0[16], v1[16];
 #pragma unroll
-                for (uint32_t j = 0; j < 8; ++j) {
+                for (uint32_t j = 0; j < 16; ++j) {
                     const uint32_t h = __builtin_elementwise_min(h0 + j, gl);
                     // workgroup h's part of slab s is its first slot unless h began in an earlier slab
                     const uint32_t si = sp.first(h) < s * nb ? 1u : 0u;
@@ -747,7 +748,7 @@ __global__ __launch_bounds__(max_wg_waves(TYPE, PAIR, PF) * 64, PF && !PAIR ? 2 
                     v1[j] = PAIR ? __hip_atomic_load(&p[64 + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
                 }
 #pragma unroll
-                for (uint32_t j = 0; j < 8; ++j)
+                for (uint32_t j = 0; j < 16; ++j)
                     if (h0 + j <= gl) {
                         r0 += v0[j];
                         r1 += v1[j];
@@ -1072,15 +1073,23 @@ int resident_waves(int layout) {
 
 // One unit per wave (the instance without PF): whole slabs per workgroup when a
 // slab has at most 16 super-blocks per row, a CU holds that many waves of the
-// instance (cu_waves) and the slabs fit one workgroup per CU, else the
-// flattened split over 4-wave workgroups.
+// instance (cu_waves) and the slabs fit one workgroup per CU; k = nb/16 (rounded
+// up) workgroups per slab when nb splits evenly and those fit one per CU (the
+// 3840 x 15360 down projection: 14.5 -> 14.2 us on MI355X against 15 workgroups
+// of 4 waves per slab); else the flattened split over 4-wave workgroups.
 GemvPlan plan_one_unit(uint32_t cols, uint32_t rows, uint32_t cus, uint32_t cu_waves) {
     GemvPlan p;
     const uint32_t nb = cols / kQK;
     p.nslabs = (rows + kRowTile - 1) / kRowTile;
+    const uint32_t k = (nb + 15) / 16;  // workgroups per slab
     if (nb <= 16 && nb <= cu_waves && p.nslabs <= cus) {
         p.W = nb;
         p.G = p.nslabs;
+    } else if (env_int("NS_GEMV_QSLAB", 1) != 0 && nb % k == 0 && nb / k <= cu_waves && p.nslabs * k <= cus) {
+        // k workgroups of nb/k waves per slab (the 60-block down projection: 4 x 15):
+        // 4 parts cross workgroups instead of 15
+        p.W = nb / k;
+        p.G = p.nslabs * k;
     } else {
         p.W = kWgWaves;
         p.G = (p.nslabs * nb + kWgWaves - 1) / kWgWaves;
