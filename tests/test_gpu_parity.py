@@ -91,6 +91,29 @@ def test_gemv(ctx, qtype, cols, rows, name, layout):
     assert rel_err(y.cpu().numpy(), ref) <= TOL32
 
 
+@pytest.mark.parametrize("qslab", ["1", "0"], ids=["k_wg_per_slab", "flattened"])
+@pytest.mark.parametrize("qtype,rows,layout", [(N.Q6_K, 3840, N.CDNA4), (N.Q4_K, 3840, N.NSMFFN),
+                                               (N.Q6_K, 3840 - 24, N.ROW_MAJOR)],
+                         ids=["q6k_cdna4", "q4k_nsmffn", "q6k_rowmajor_ragged"])
+def test_down_plans(ctx, monkeypatch, qslab, qtype, rows, layout):
+    """The 60-block down projection under both grids of the one-unit instance:
+    4 workgroups of 15 waves per slab (default) and the flattened split
+    (NS_GEMV_QSLAB=0, 15 workgroups per slab); both meet the bar and repeat."""
+    monkeypatch.setenv("NS_GEMV_QSLAB", qslab)
+    cols = 15360
+    host, w = weights(qtype, 41, rows, cols, layout)
+    x = f32(cols, 42)
+    ref = O.gemv(qtype, O.ROW_MAJOR, host, cols, rows, x)
+    ys = []
+    for _ in range(2):
+        y = torch.empty(rows, dtype=torch.float32, device="cuda")
+        ctx.matmul(w, qtype, layout, cols, rows, 1, torch.from_numpy(x).cuda(), y)
+        ys.append(y)
+    torch.cuda.synchronize()
+    assert rel_err(ys[0].cpu().numpy(), ref) <= TOL32
+    assert torch.equal(ys[0], ys[1])
+
+
 @pytest.mark.parametrize("layout", [N.CDNA4, N.ROW_MAJOR], ids=LNAME.get)
 def test_lm_head_gemv(ctx, layout):
     """Config 1b: Q6_K 262144 x 3840 lm-head (row-major in the reference, mm:576)."""
