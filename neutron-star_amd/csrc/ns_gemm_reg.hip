@@ -246,12 +246,14 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
                 decode8(raw[ri][j].qa, slo[j], shi[j], fb[j].f[0], fb[j].f[2]);
                 decode8(raw[ri][j].qb, slo[j], shi[j], fb[j].f[1], fb[j].f[3]);
             }
-            __builtin_amdgcn_sched_barrier(0);
+            // No scheduling fence around the decode, the loads and the MFMAs: the
+            // scheduler may move decode and rescale work between the MFMAs (MI355X,
+            // gate/up pair at batch 1024: 1-3% faster than with fences).  The loads
+            // of s+2 overwrite raw(s)'s registers, so they follow its decode anyway.
             if (s + 2 < send) {
                 dma_x(s + 2, (s + 2) % XBUF);
                 load_raw(s + 2, raw[ri]);
             }
-            __builtin_amdgcn_sched_barrier(0);
             if (jstep == 0 && sb > sb0) {
 #pragma unroll
                 for (int j = 0; j < NJ; ++j) {
