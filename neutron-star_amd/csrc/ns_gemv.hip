@@ -6,12 +6,14 @@
 //
 // Work decomposition (wave64, lane = weight row):
 //   * the work is the flattened sequence of (64-row slab, super-block) units;
-//     the grid holds as many workgroups as the device keeps resident, each
-//     takes an equal contiguous run of units and splits it evenly over its
-//     waves, so every wave streams the same number of weight bytes;
+//     each workgroup takes an equal contiguous run of units and splits it
+//     evenly over its waves.  The grid (plan_gemv, plan_one_unit) is one slab
+//     per 4-wave workgroup for the streaming lm-head, one workgroup (or k) per
+//     slab for the one-unit-per-wave instance, else the resident workgroups;
 //   * every lane streams its own row's blocks: in the CDNA4 layout each of the
 //     9 (Q4_K) or 13 (Q6_K) 16-byte chunk loads of a wave is one contiguous
-//     1 KiB transaction; the next unit is prefetched while one is computed;
+//     1 KiB transaction; the streaming instance prefetches the next unit into a
+//     second register buffer while one is computed;
 //   * x is wave-uniform (every lane needs the same 256 values of a block) and
 //     is read with scalar loads; per-group sums of x are built across lanes;
 //   * a wave writes the slabs it covers whole; slabs cut between waves meet in
