@@ -68,9 +68,25 @@ int ns_abi_version(void);
 
 /* Context on HIP device `device`: owns the split-reduction workspace
  * (the engine's workspaces, mm:100-101).  No counterpart function in the
- * reference (the engine constructor does this, mm:90-133). */
+ * reference (the engine constructor does this, mm:90-133).  The workspace is
+ * sized at creation for every FFN shape of the reference model (model.cpp:14-19)
+ * in every layout up to batch 2048 (config.cpp:124), so those calls never
+ * allocate.  Another shape that needs more grows it: new buffers are
+ * allocated and the old ones kept until ns_ctx_destroy (queued work and
+ * captured graphs may still use them); growth never synchronises and fails
+ * with NS_ERR_UNSUPPORTED while the call's stream is capturing a graph. */
 int ns_ctx_create(int device, ns_ctx **out);
 int ns_ctx_destroy(ns_ctx *ctx);
+/* Bytes of device workspace the context holds now. */
+int ns_ctx_workspace_bytes(const ns_ctx *ctx, uint64_t *bytes);
+/* Test and experiment hook, no counterpart in the reference: overrides one
+ * kernel-selection choice of this context.  Keys: "gemv_pf" (-1 plan, 0 / 1
+ * force the one-unit / prefetching decode GEMV), "gemv_waves" (> 0: the
+ * prefetching GEMV's flattened grid), "gemv_whole" / "gemv_qslab" (0 disables
+ * that decode grid), "gemm_kparts" (> 0: split-K parts of the prefill GEMM),
+ * "gemm_q4_reg" (0: the LDS-tile Q4_K GEMM).  Results stay within the same
+ * tolerances; engines leave the defaults. */
+int ns_ctx_set_tuning(ns_ctx *ctx, const char *key, int value);
 
 /* NativeMetalEngine::matmul (mm:269-275): out = in . W^T for `batch` tokens.
  *   batch == 1, fp32 input      -> dequant-fused GEMV (decode; lm-head with ROW_MAJOR or CDNA4).
@@ -124,8 +140,9 @@ int ns_dequant(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, 
  *   ns_rmsnorm_add_then: y as ns_rmsnorm_add, then next = (y*r2)*next_weight with r2 taken
  *                        over y, as fp16 bits (half_next: rms_add_then_half) or fp32 (rms_add
  *                        followed by rms, the decode order at mm:563).
- * Device pointers; scale points at one fp32 (a layer's out_scale tensor).  y may alias x or
- * residual (each element is read before it is written, by the same thread). */
+ * Device pointers; scale points at one fp32 (a layer's out_scale tensor).  An fp32 y may
+ * alias x or residual of the same shape (every element is read before it is written, by the
+ * thread that writes it); fp16 outputs and `next` must not overlap any input. */
 int ns_rmsnorm(ns_ctx *ctx, const float *x, const float *weight, uint32_t rows, uint32_t width, float eps,
                void *y, int half_out, void *stream);
 int ns_rmsnorm_add(ns_ctx *ctx, const float *x, const float *weight, const float *residual, const float *scale,

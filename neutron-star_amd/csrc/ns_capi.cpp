@@ -10,9 +10,14 @@
 #include "ns_ffn.h"
 #include "ns_internal.hpp"
 
+#include <vector>
+
 struct ns_ctx {
     int device = 0;
     ns::Workspace ws;
+    // Buffers replaced by workspace growth.  Work queued earlier, or a graph
+    // captured earlier, may still use them, so they live until ns_ctx_destroy.
+    std::vector<void *> retired;
 };
 
 namespace {
@@ -39,41 +44,92 @@ int check_tensor(const char *fn, const void *w, int type, int layout, uint32_t c
     const uintptr_t a = reinterpret_cast<uintptr_t>(w);
     if ((type == Q4_K && a % 16) || (type == Q6_K && a % 4))
         return fail(NS_ERR_ARG, std::string(fn) + ": weight pointer misaligned");
+    // The kernels address a tensor through buffer descriptors with a 32-bit byte range.
+    if (uint64_t(rows) * (cols / kQK) * block_bytes(type) >= (uint64_t(1) << 31))
+        return fail(NS_ERR_SHAPE, std::string(fn) + ": tensor of 2 GiB or more");
     return NS_OK;
 }
 
-// Grows the context workspace; the old buffers may still be read by queued
-// work, so the device is drained first (growth happens once per new shape).
-int ensure_ws(ns_ctx *ctx, size_t partial_floats, size_t counters) {
+// Makes the context workspace hold at least this much.  ns_ctx_create sizes it
+// for every FFN shape of the reference model up to batch 2048, so growth is for
+// other shapes only.  Growth allocates new buffers and retires the old ones
+// without freeing them (queued work and captured graphs may still use them), so
+// it never synchronises; it is refused while `s` is capturing a graph, where an
+// allocation cannot be recorded.
+int ensure_ws(ns_ctx *ctx, size_t partial_floats, size_t counters, hipStream_t s) {
     if (partial_floats <= ctx->ws.partial_floats && counters <= ctx->ws.counter_count) return NS_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (s && hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+        return fail(NS_ERR_UNSUPPORTED, "workspace growth during stream capture: run the shape once before capturing");
     hipError_t e = hipSetDevice(ctx->device);
-    if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) return hip_fail(e, "workspace growth");
     if (partial_floats > ctx->ws.partial_floats) {
-        if (ctx->ws.partial) (void)hipFree(ctx->ws.partial);
-        ctx->ws.partial = nullptr;
-        ctx->ws.partial_floats = 0;
-        e = hipMalloc(reinterpret_cast<void **>(&ctx->ws.partial), partial_floats * sizeof(float));
+        float *p = nullptr;
+        e = hipMalloc(reinterpret_cast<void **>(&p), partial_floats * sizeof(float));
         if (e != hipSuccess) return hip_fail(e, "workspace allocation");
+        if (ctx->ws.partial) ctx->retired.push_back(ctx->ws.partial);
+        ctx->ws.partial = p;
         ctx->ws.partial_floats = partial_floats;
     }
     if (counters > ctx->ws.counter_count) {
-        if (ctx->ws.counters) (void)hipFree(ctx->ws.counters);
-        ctx->ws.counters = nullptr;
-        ctx->ws.counter_count = 0;
-        e = hipMalloc(reinterpret_cast<void **>(&ctx->ws.counters), counters * sizeof(uint32_t));
-        if (e == hipSuccess) e = hipMemset(ctx->ws.counters, 0, counters * sizeof(uint32_t));
+        uint32_t *c = nullptr;
+        e = hipMalloc(reinterpret_cast<void **>(&c), counters * sizeof(uint32_t));
         if (e != hipSuccess) return hip_fail(e, "workspace allocation");
+        // stream-ordered before the first kernel that counts in it
+        e = hipMemsetAsync(c, 0, counters * sizeof(uint32_t), s);
+        if (e != hipSuccess) {
+            (void)hipFree(c);
+            return hip_fail(e, "workspace allocation");
+        }
+        if (ctx->ws.counters) ctx->retired.push_back(ctx->ws.counters);
+        ctx->ws.counters = c;
         ctx->ws.counter_count = counters;
     }
     return NS_OK;
 }
 
+// Workspace every FFN call of the reference model needs (model.cpp:14-19: gate/up
+// 15360 x 3840 Q4_K, down 3840 x 15360 Q4_K or Q6_K, lm-head 262144 x 3840 Q6_K) in
+// every layout, for every batch the engine allows (1..2048, config.cpp:124).
+void model_workspace_need(const Tuning &t, size_t *floats, size_t *counters) {
+    size_t pf = 0, nc = 0;
+    auto take = [&](size_t f, size_t c) {
+        pf = std::max(pf, f);
+        nc = std::max(nc, c);
+    };
+    struct Shape {
+        int type;
+        uint32_t cols, rows;
+        bool pair;
+    };
+    const Shape shapes[] = {{Q4_K, 3840, 15360, true}, {Q4_K, 3840, 15360, false}, {Q4_K, 15360, 3840, false},
+                            {Q6_K, 15360, 3840, false}, {Q6_K, 3840, 262144, false}};
+    for (int layout : {ROW_MAJOR, NSMFFN, CDNA4})
+        for (const Shape &sh : shapes) {
+            size_t f = 0, c = 0;
+            gemv_workspace_need(sh.type, layout, sh.cols, sh.rows, sh.pair, t, &f, &c);
+            take(f, c);
+            for (uint32_t b = 2; b <= 4; ++b)
+                for (bool xh : {false, true}) {
+                    if (sh.pair && !xh) continue;
+                    gemv_mt_workspace_need(sh.type, layout, sh.cols, sh.rows, sh.pair, b, xh, t, &f, &c);
+                    take(f, c);
+                }
+            if (sh.rows > 16384) continue;  // the lm-head is a decode GEMV
+            for (uint32_t b = 5; b <= 2048; ++b) {
+                gemm_workspace_need(sh.type, layout, sh.cols, sh.rows, b, sh.pair, t, &f, &c);
+                take(f, c);
+            }
+        }
+    *floats = pf;
+    *counters = nc;
+}
+
 int gemv(ns_ctx *ctx, const char *fn, int type, int layout, const void *w, const void *up, const float *x,
          float *out, uint32_t cols, uint32_t rows, hipStream_t s) {
     size_t pf = 0, nc = 0;
-    gemv_workspace_need(type, layout, cols, rows, up != nullptr, &pf, &nc);
-    if (int rc = ensure_ws(ctx, pf, nc)) return rc;
+    gemv_workspace_need(type, layout, cols, rows, up != nullptr, ctx->ws.tune, &pf, &nc);
+    if (int rc = ensure_ws(ctx, pf, nc, s)) return rc;
     const hipError_t e = launch_gemv(type, layout, static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(up),
                                      x, out, cols, rows, ctx->ws, s);
     return e == hipSuccess ? NS_OK : hip_fail(e, fn);
@@ -83,8 +139,8 @@ int gemv(ns_ctx *ctx, const char *fn, int type, int layout, const void *w, const
 int gemv_mt(ns_ctx *ctx, const char *fn, int type, int layout, const void *w, const void *up, const void *x,
             bool xh, uint32_t batch, void *out, uint32_t cols, uint32_t rows, hipStream_t s) {
     size_t pf = 0, nc = 0;
-    gemv_mt_workspace_need(type, layout, cols, rows, up != nullptr, batch, xh, &pf, &nc);
-    if (int rc = ensure_ws(ctx, pf, nc)) return rc;
+    gemv_mt_workspace_need(type, layout, cols, rows, up != nullptr, batch, xh, ctx->ws.tune, &pf, &nc);
+    if (int rc = ensure_ws(ctx, pf, nc, s)) return rc;
     const hipError_t e = launch_gemv_mt(type, layout, static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(up),
                                         x, xh, batch, out, cols, rows, ctx->ws, s);
     return e == hipSuccess ? NS_OK : hip_fail(e, fn);
@@ -93,8 +149,8 @@ int gemv_mt(ns_ctx *ctx, const char *fn, int type, int layout, const void *w, co
 int gemm(ns_ctx *ctx, const char *fn, int type, int layout, int acc, const void *w, const void *up,
          const uint16_t *x, void *out, uint32_t cols, uint32_t rows, uint32_t batch, hipStream_t s) {
     size_t wf = 0, wc = 0;
-    gemm_workspace_need(type, layout, cols, rows, batch, up != nullptr, &wf, &wc);
-    if (int rc = ensure_ws(ctx, wf, wc)) return rc;
+    gemm_workspace_need(type, layout, cols, rows, batch, up != nullptr, ctx->ws.tune, &wf, &wc);
+    if (int rc = ensure_ws(ctx, wf, wc, s)) return rc;
     const hipError_t e = launch_gemm(type, layout, acc, static_cast<const uint8_t *>(w),
                                      static_cast<const uint8_t *>(up), x, out, cols, rows, batch, ctx->ws, s);
     return e == hipSuccess ? NS_OK : hip_fail(e, fn);
@@ -113,12 +169,39 @@ extern "C" int ns_ctx_create(int device, ns_ctx **out) {
     if (e != hipSuccess) return hip_fail(e, "ns_ctx_create");
     auto *ctx = new ns_ctx;
     ctx->device = device;
-    // Enough for every shape of the supported model without growth.
-    if (int rc = ensure_ws(ctx, size_t(8) << 20, size_t(1) << 16)) {
+    // Enough for every FFN shape of the reference model without growth.
+    size_t pf = 0, nc = 0;
+    model_workspace_need(ctx->ws.tune, &pf, &nc);
+    if (int rc = ensure_ws(ctx, pf, std::max(nc, size_t(1) << 16), nullptr)) {
         ns_ctx_destroy(ctx);
         return rc;
     }
+    e = hipDeviceSynchronize();  // the counters' clear has finished before any stream uses them
+    if (e != hipSuccess) {
+        ns_ctx_destroy(ctx);
+        return hip_fail(e, "ns_ctx_create");
+    }
     *out = ctx;
+    return NS_OK;
+}
+
+extern "C" int ns_ctx_workspace_bytes(const ns_ctx *ctx, uint64_t *bytes) {
+    if (!ctx || !bytes) return fail(NS_ERR_ARG, "ns_ctx_workspace_bytes: null argument");
+    *bytes = uint64_t(ctx->ws.partial_floats) * sizeof(float) + uint64_t(ctx->ws.counter_count) * sizeof(uint32_t);
+    return NS_OK;
+}
+
+extern "C" int ns_ctx_set_tuning(ns_ctx *ctx, const char *key, int value) {
+    if (!ctx || !key) return fail(NS_ERR_ARG, "ns_ctx_set_tuning: null argument");
+    Tuning &t = ctx->ws.tune;
+    const std::string k(key);
+    if (k == "gemv_pf") t.gemv_pf = value;
+    else if (k == "gemv_waves") t.gemv_waves = value;
+    else if (k == "gemv_whole") t.gemv_whole = value;
+    else if (k == "gemv_qslab") t.gemv_qslab = value;
+    else if (k == "gemm_kparts") t.gemm_kparts = value;
+    else if (k == "gemm_q4_reg") t.gemm_q4_reg = value;
+    else return fail(NS_ERR_ARG, "ns_ctx_set_tuning: unknown key " + k);
     return NS_OK;
 }
 
@@ -128,6 +211,7 @@ extern "C" int ns_ctx_destroy(ns_ctx *ctx) {
     (void)hipDeviceSynchronize();
     if (ctx->ws.partial) (void)hipFree(ctx->ws.partial);
     if (ctx->ws.counters) (void)hipFree(ctx->ws.counters);
+    for (void *p : ctx->retired) (void)hipFree(p);
     delete ctx;
     return NS_OK;
 }
@@ -260,8 +344,8 @@ int rms_gate_up(ns_ctx *ctx, const char *fn, const void *wg, const void *wu, int
     if ((reinterpret_cast<uintptr_t>(np.x) | reinterpret_cast<uintptr_t>(np.wb)) % 16)
         return fail(NS_ERR_ARG, std::string(fn) + ": x and norm_weight must be 16-byte aligned");
     size_t pf = 0, nc = 0;
-    gemv_workspace_need(Q4_K, layout, cols, rows, true, &pf, &nc);
-    if (int rc = ensure_ws(ctx, pf, nc)) return rc;
+    gemv_workspace_need(Q4_K, layout, cols, rows, true, ctx->ws.tune, &pf, &nc);
+    if (int rc = ensure_ws(ctx, pf, nc, static_cast<hipStream_t>(stream))) return rc;
     const hipError_t e = launch_gemv(Q4_K, layout, static_cast<const uint8_t *>(wg), static_cast<const uint8_t *>(wu),
                                      nullptr, h, cols, rows, ctx->ws, static_cast<hipStream_t>(stream), &np);
     return e == hipSuccess ? NS_OK : hip_fail(e, fn);

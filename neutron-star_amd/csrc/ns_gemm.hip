@@ -32,15 +32,19 @@
 // on XCD i % 8), so each XCD's L2 keeps its own 128 x K slice of x.
 //
 // Accumulation modes (metal_engine.mm:565):
-//   FP32  Y accumulates in fp32.
-//   FP16  Y is rounded to fp16 precision (11 significant bits, fp32 exponent
-//         range) after every super-block update, so outputs carry fp16
-//         precision (metal:394/:489 widen half tiles).  True fp16 range would
+//   FP32  the exact integer tiles above, Y accumulated in fp32.
+//   FP16  the reference's fp16 weight tiles with a per-row power-of-two scale
+//         (ns_tile16.hpp; no rescale, no min-term MFMAs), Y accumulated in fp32
+//         and rounded once to fp16 precision (11 significant bits, fp32 exponent
+//         range; metal:394/:489 write a half tile).  True fp16 range would
 //         overflow on BASELINE's synthetic inputs (down outputs reach 1.7e5).
+//         The CDNA4 layout runs this mode in ns_gemm_f16.hip.
+#include <algorithm>
 #include <type_traits>
 
 #include "ns_internal.hpp"
 #include "ns_quant.hpp"
+#include "ns_tile16.hpp"
 
 namespace ns {
 namespace {
@@ -214,6 +218,46 @@ __device__ __forceinline__ void decode(const RawQ6 &r, uint32_t s, uint32_t hh, 
     }
 }
 
+// FP16-mode tiles (ns_tile16.hpp): F = RNE16(q*2^-24*A + B) with the row scale in
+// c24 = c * 2^24; same element placement as the exact decode above.
+__device__ __forceinline__ void decode_f16(const RawQ4 &r, uint32_t s, float c24, WRun &out) {
+    const uint32_t p = s & 3;
+    const float d = lo_half(r.hdr.x), dmin = hi_half(r.hdr.x);
+    const Q4Scales sc = q4_scales(r.hdr.y, r.hdr.z, r.hdr.w);
+    const float dc = d * c24, mc = -dmin * (c24 * 5.9604644775390625e-08f);
+    const half2_t Alo = splat(_Float16(dc * float(q4_sc(sc, int(2 * p))))), Ahi = splat(_Float16(dc * float(q4_sc(sc, int(2 * p + 1)))));
+    const half2_t Blo = splat(_Float16(mc * float(q4_m(sc, int(2 * p))))), Bhi = splat(_Float16(mc * float(q4_m(sc, int(2 * p + 1)))));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t lo[2], hi[2];
+        q4_f16x8(r.qs[i], Alo, Blo, Ahi, Bhi, lo, hi);
+        out.v[i >> 1][(i & 1) * 2 + 0] = lo[0];
+        out.v[i >> 1][(i & 1) * 2 + 1] = lo[1];
+        out.v[2 + (i >> 1)][(i & 1) * 2 + 0] = hi[0];
+        out.v[2 + (i >> 1)][(i & 1) * 2 + 1] = hi[1];
+    }
+}
+__device__ __forceinline__ void decode_f16(const RawQ6 &r, uint32_t s, uint32_t hh, float c24, WRun &out) {
+    const uint32_t sr = s & 3, h = sr >> 1, qa = 2 * (sr & 1) + hh;
+    const uint32_t si = 8 * h + 2 * qa;
+    const uint32_t nshift = qa >= 2 ? 4 : 0, hshift = 2 * qa;
+    const float d = lo_half(r.dbits);
+    const float dc = d * c24, dm = -32.0f * d * (c24 * 5.9604644775390625e-08f);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {  // l = 16c .. 16c+15
+        const float scf = float(int(int8_t(byte_of(r.scw[(si + c) >> 2], int((si + c) & 3)))));
+        const half2_t A = splat(_Float16(dc * scf)), B = splat(_Float16(dm * scf));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {  // l = 16c + 4i .. +3
+            const uint32_t v = ((r.ql[c][i] >> nshift) & 0x0F0F0F0Fu) | (((r.qh[c][i] >> hshift) & 0x03030303u) << 4);
+            uint32_t o[2];
+            q6_f16x4(v, A, B, o);
+            out.v[2 * c + (i >> 1)][(i & 1) * 2 + 0] = o[0];
+            out.v[2 * c + (i >> 1)][(i & 1) * 2 + 1] = o[1];
+        }
+    }
+}
+
 // Running sum in one accumulator.  Within super-block sb the MFMA accumulator
 // holds S/e_sb, where S is the running sum of the output and e_sb is a per-row
 // factor: e = d for Q6_K; e = max(d, dmin/1024) for Q4_K (e = 1 if that is 0).
@@ -251,10 +295,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     uint32_t *__restrict__ counters, uint32_t cols, uint32_t rows, uint32_t batch, uint32_t ntok_tiles,
     uint32_t ncol_tiles, uint32_t kparts_total, uint32_t wbytes) {
     constexpr bool Q4 = TYPE == Q4_K;
+    constexpr bool F16 = ACC == ACC_FP16;  // fp16 tiles (ns_tile16.hpp) instead of exact ones
     constexpr uint32_t kRawLoads = Q4 ? 2 : (LAYOUT == CDNA4 ? 6 : 41);  // vector loads per load_raw
     __shared__ __attribute__((aligned(16))) _Float16 Ws[2][TC * LDSW];
     __shared__ __attribute__((aligned(16))) u32x4 Xs[2][TT * 8];
     __shared__ float colE[2][TC];
+    __shared__ float colInv[TC];  // FP16 mode: 1/c of each column's row
     // Q4_K min factors per column: 8 fp16 values b_g, then their 8 rounding residues
     __shared__ __attribute__((aligned(16))) _Float16 colB[2][Q4 ? TC * 16 : 16];
     __shared__ uint32_t last_flag;
@@ -286,7 +332,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     const rsrc_t xsrc = make_rsrc(x, batch * cols * 2);
     // x group sums: plane hi [batch][ngroups] then plane lo; rows past batch are
     // never stored, so their (lo-plane) contents do not matter
-    const rsrc_t xssrc = make_rsrc(xsums, Q4 ? 2 * batch * ngroups * 2 : 0);
+    const rsrc_t xssrc = make_rsrc(xsums, (Q4 && !F16) ? 2 * batch * ngroups * 2 : 0);
 
     float16_t acc[MI][NJ];
 #pragma unroll
@@ -318,6 +364,24 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     Raw<TYPE> raw[2] = {};
     u32x4 xsf[MI] = {};  // Q4_K: group sums of x for this super-block (hi in lanes 0-31, lo in 32-63)
 
+    // FP16 mode: the row scale of this producer's column (rows past `rows` read zeros: c = 1)
+    float c24 = 0.f;
+    if constexpr (F16) {
+        float M = 0.f;
+        for (uint32_t b = 0; b < nb; ++b) {
+            if constexpr (Q4) {
+                const uint32_t off = uint32_t(byte_offset(TYPE, LAYOUT, wrow, b, nb, 0));
+                const uint32_t dd = bload2(wsrc, off) | (bload2(wsrc, off + 2) << 16);
+                M = __builtin_fmaxf(M, __builtin_fmaxf(__builtin_fabsf(lo_half(dd)), __builtin_fabsf(hi_half(dd))));
+            } else {
+                M = __builtin_fmaxf(M, __builtin_fabsf(lo_half(bload2(wsrc, uint32_t(byte_offset(TYPE, LAYOUT, wrow, b, nb, 208))))));
+            }
+        }
+        float inv_c;
+        row_scale(M, c24, inv_c);
+        if (hh == 0) colInv[wc] = inv_c;
+    }
+
     // Decode raw weights of step s into weight buffer s&1 (and, on the first step
     // of a super-block, its per-row factors).
     auto produce = [&](uint32_t s, const Raw<TYPE> &rw) {
@@ -334,13 +398,18 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
         const float re = __builtin_amdgcn_rcpf(e);  // ~1 ulp; exactness is kept by z = 1 when e == d
         const float z = d == e ? 1.f : d * re;
         WRun wr;
-        decode(rw, s, hh, z, wr);
+        if constexpr (F16) {
+            if constexpr (Q4) decode_f16(rw, s, c24, wr);
+            else decode_f16(rw, s, hh, c24, wr);
+        } else {
+            decode(rw, s, hh, z, wr);
+        }
         _Float16 *wl = &Ws[buf][wc * LDSW];
         *reinterpret_cast<u32x4 *>(wl + k_lo(TYPE, hh)) = wr.v[0];
         *reinterpret_cast<u32x4 *>(wl + k_lo(TYPE, hh) + 8) = wr.v[1];
         *reinterpret_cast<u32x4 *>(wl + k_hi(TYPE, hh)) = wr.v[2];
         *reinterpret_cast<u32x4 *>(wl + k_hi(TYPE, hh) + 8) = wr.v[3];
-        if ((s & 3) == 0 && hh == 0) {
+        if (!F16 && (s & 3) == 0 && hh == 0) {
             colE[pb][wc] = e;
             if constexpr (Q4) {
                 const float f = -hi_half(rw.hdr.x) * re;
@@ -382,7 +451,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
         for (int j = 0; j < 4; ++j) {
             const uint32_t s = 4 * sb + uint32_t(j), buf = uint32_t(j) & 1;
             const bool more = s + 1 < 4 * sb1;
-            if constexpr (Q4) {
+            if constexpr (Q4 && !F16) {
                 if (j == 0) {
 #pragma unroll
                     for (int i = 0; i < MI; ++i)
@@ -393,7 +462,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
             if (more) dma_x(s + 1, buf ^ 1);
             load_w(s + 2, raw[j & 1]);  // slot of raw(s), decoded during step s-1
 
-            if (j == 0 && sb > sb0) {  // enter super-block sb: S/e_prev -> S/e_sb
+            if (!F16 && j == 0 && sb > sb0) {  // enter super-block sb: S/e_prev -> S/e_sb
 #pragma unroll
                 for (int jj = 0; jj < NJ; ++jj) {
                     const uint32_t c = bcol(jj) + (lane & 31);
@@ -403,8 +472,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
                     for (int i = 0; i < MI; ++i)
 #pragma unroll
                         for (int v = 0; v < 16; ++v) {
-                            if constexpr (ACC == ACC_FP16) acc[i][jj][v] = round_f16p(acc[i][jj][v] * e_prev) * rinv;
-                            else acc[i][jj][v] *= r;
+                            acc[i][jj][v] *= r;
                         }
                 }
             }
@@ -436,7 +504,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
                 if (kk == 1 && more) produce(s + 1, raw[(j + 1) & 1]);
             }
 
-            if constexpr (Q4) {
+            if constexpr (Q4 && !F16) {
                 if (j == 3) {  // min term of super-block sb
                     // b_g in k 0-7 (hi sums) and k 8-15 (lo sums); the residues of b_g in k 0-7
                     // only (against the hi sums), so the min term keeps ~22 significant bits
@@ -466,14 +534,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     const uint32_t pl = (sb1 - 1 - sb0) & 1;
 #pragma unroll
     for (int jj = 0; jj < NJ; ++jj) {
-        const float el = colE[pl][bcol(jj) + (lane & 31)];
+        // FP16 mode: the tiles carry the row scale c, so S = acc / c
+        const float el = F16 ? colInv[bcol(jj) + (lane & 31)] : colE[pl][bcol(jj) + (lane & 31)];
 #pragma unroll
         for (int i = 0; i < MI; ++i)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                acc[i][jj][v] *= el;
-                if constexpr (ACC == ACC_FP16) acc[i][jj][v] = round_f16p(acc[i][jj][v]);
-            }
+            for (int v = 0; v < 16; ++v) acc[i][jj][v] *= el;
     }
     auto tok_of = [&](int i, int v) -> uint32_t {
         return t0 + wt * WT + uint32_t(i) * 32 + 8 * uint32_t(v >> 2) + 4 * (lane >> 5) + uint32_t(v & 3);
@@ -504,9 +570,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
         }
     };
 
+    // FP16 mode rounds the finished sum once: here, or after the split-K parts are added
     if (kparts == 1) {
 #pragma unroll
-        for (int i = 0; i < MI; ++i) write_out(i, [&](int v, int jj) { return acc[i][jj][v]; });
+        for (int i = 0; i < MI; ++i)
+            write_out(i, [&](int v, int jj) { return ACC == ACC_FP16 ? round_f16p(acc[i][jj][v]) : acc[i][jj][v]; });
         return;
     }
 
@@ -617,7 +685,7 @@ struct GemmPlan {
 
 // Output tiles and split of K: enough workgroups to cover most of the 256 CUs
 // (the 3840-row down projection has only 4 x 15 tiles at batch 1024).
-GemmPlan plan_gemm(uint32_t cols, uint32_t rows, uint32_t batch, bool pair) {
+GemmPlan plan_gemm(uint32_t cols, uint32_t rows, uint32_t batch, bool pair, const Tuning &t) {
     GemmPlan p;
     p.ntok = (batch + TT - 1) / TT;
     const uint32_t rows_per_tile = pair ? TC / 2 : TC;
@@ -625,10 +693,7 @@ GemmPlan plan_gemm(uint32_t cols, uint32_t rows, uint32_t batch, bool pair) {
     const uint32_t nb = cols / kQK, tiles = p.ntok * p.ncol;
     p.kparts = 1;
     while (tiles * p.kparts < 200 && p.kparts * 2 <= nb / 4) p.kparts *= 2;
-    if (const char *e = getenv("NS_GEMM_KPARTS"); e && *e) {
-        const int v = atoi(e);
-        if (v >= 1 && uint32_t(v) <= nb) p.kparts = uint32_t(v);
-    }
+    if (t.gemm_kparts >= 1 && uint32_t(t.gemm_kparts) <= nb) p.kparts = uint32_t(t.gemm_kparts);
     // one split-K part (padded to whole tiles) must stay under 4 GiB: 32-bit offsets in the kernel
     if (uint64_t(pair ? 2 : 1) * p.ntok * TT * p.ncol * rows_per_tile * 4 >= (uint64_t(1) << 32)) p.kparts = 1;
     return p;
@@ -638,7 +703,7 @@ template <int TYPE, int LAYOUT, bool PAIR>
 hipError_t launch_mode(int acc, const uint8_t *w, const uint8_t *up, const uint16_t *x, const uint16_t *xh,
                        void *out, uint32_t cols, uint32_t rows, uint32_t batch, const Workspace &ws,
                        size_t ws_offset, hipStream_t stream) {
-    const GemmPlan p = plan_gemm(cols, rows, batch, PAIR);
+    const GemmPlan p = plan_gemm(cols, rows, batch, PAIR, ws.tune);
     const dim3 grid(p.ntok * p.ncol * p.kparts), block(kThreads);
     const uint32_t wbytes = rows * (cols / kQK) * block_bytes(TYPE);
     float *partial = ws.partial + ws_offset;
@@ -671,23 +736,35 @@ static size_t xs_floats(int type, uint32_t cols, uint32_t batch) {
     return type == Q4_K ? ((size_t(batch) * (cols / 32) + 63) / 64) * 64 : 0;
 }
 
+static void gemm_fp32_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, uint32_t batch, bool pair,
+                                     const Tuning &t, size_t *floats, size_t *counters);
+
 // Q4_K on the CDNA4 layout runs the register-fragment kernel (ns_gemm_reg.hip)
-// unless NS_GEMM_Q4_REG=0 selects the LDS-tile kernel here.
-static bool use_gemm_reg(int type, int layout) {
-    if (layout != CDNA4 || type != Q4_K) return false;
-    const char *e = getenv("NS_GEMM_Q4_REG");
-    return !(e && e[0] == '0');
+// unless Tuning::gemm_q4_reg = 0 selects the LDS-tile kernel here.
+static bool use_gemm_reg(int type, int layout, const Tuning &t) {
+    return layout == CDNA4 && type == Q4_K && t.gemm_q4_reg != 0;
 }
 
 void gemm_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, uint32_t batch, bool pair,
-                         size_t *floats, size_t *counters) {
-    if (use_gemm_reg(type, layout)) {
+                         const Tuning &t, size_t *floats, size_t *counters) {
+    // FP16 mode on CDNA4 runs ns_gemm_f16.hip; the need covers both modes
+    size_t f16_floats = 0, f16_counters = 0;
+    if (layout == CDNA4) gemm_f16_workspace_need(cols, rows, batch, pair, t, &f16_floats, &f16_counters);
+    size_t f32_floats = 0, f32_counters = 0;
+    gemm_fp32_workspace_need(type, layout, cols, rows, batch, pair, t, &f32_floats, &f32_counters);
+    *floats = std::max(f16_floats, f32_floats);
+    *counters = std::max(f16_counters, f32_counters);
+}
+
+static void gemm_fp32_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, uint32_t batch, bool pair,
+                                     const Tuning &t, size_t *floats, size_t *counters) {
+    if (use_gemm_reg(type, layout, t)) {
         size_t part = 0;
-        gemm_reg_workspace_need(cols, rows, batch, pair, &part, counters);
+        gemm_reg_workspace_need(cols, rows, batch, pair, t, &part, counters);
         *floats = xs_floats(type, cols, batch) + part;
         return;
     }
-    const GemmPlan p = plan_gemm(cols, rows, batch, pair);
+    const GemmPlan p = plan_gemm(cols, rows, batch, pair, t);
     *floats = xs_floats(type, cols, batch) +
               (p.kparts > 1 ? size_t(p.kparts) * (pair ? 2 : 1) * (p.ntok * TT) * (p.ncol * (pair ? TC / 2 : TC)) : 0);
     *counters = size_t(p.ntok) * p.ncol;
@@ -696,8 +773,10 @@ void gemm_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, uin
 hipError_t launch_gemm(int type, int layout, int acc, const uint8_t *w, const uint8_t *up, const uint16_t *x,
                        void *out, uint32_t cols, uint32_t rows, uint32_t batch, const Workspace &ws,
                        hipStream_t stream) {
+    if (layout == CDNA4 && acc == ACC_FP16)
+        return launch_gemm_f16(type, w, up, x, out, cols, rows, batch, ws.partial, ws.counters, ws.tune, stream);
     uint16_t *xh = nullptr, *xl = nullptr;
-    if (type == Q4_K) {
+    if (type == Q4_K && acc == ACC_FP32) {  // the exact tiles' min term needs the group sums of x
         const size_t n = size_t(batch) * (cols / 32);
         xh = reinterpret_cast<uint16_t *>(ws.partial);
         xl = xh + n;
@@ -705,8 +784,9 @@ hipError_t launch_gemm(int type, int layout, int acc, const uint8_t *w, const ui
         if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     }
     const size_t off = xs_floats(type, cols, batch);
-    if (use_gemm_reg(type, layout))
-        return launch_gemm_reg(acc, w, up, x, xh, out, cols, rows, batch, ws.partial + off, ws.counters, stream);
+    if (use_gemm_reg(type, layout, ws.tune))
+        return launch_gemm_reg(acc, w, up, x, xh, out, cols, rows, batch, ws.partial + off, ws.counters, ws.tune,
+                               stream);
     if (up) return launch_layout<Q4_K, true>(layout, acc, w, up, x, xh, out, cols, rows, batch, ws, off, stream);
     if (type == Q4_K)
         return launch_layout<Q4_K, false>(layout, acc, w, nullptr, x, xh, out, cols, rows, batch, ws, off, stream);

@@ -441,7 +441,7 @@ struct RegPlan {
     uint32_t ntok, ncol, kparts;
 };
 
-RegPlan plan_reg(uint32_t cols, uint32_t rows, uint32_t batch, bool pair) {
+RegPlan plan_reg(uint32_t cols, uint32_t rows, uint32_t batch, bool pair, const Tuning &t) {
     RegPlan p;
     p.ntok = (batch + TT - 1) / TT;
     const uint32_t rows_per_tile = pair ? TC / 2 : TC;
@@ -450,10 +450,7 @@ RegPlan plan_reg(uint32_t cols, uint32_t rows, uint32_t batch, bool pair) {
     p.kparts = 1;
     // two workgroups per CU on 256 CUs: split K until the grid covers most of them
     while (tiles * p.kparts < 400 && p.kparts * 2 <= nb / 2) p.kparts *= 2;
-    if (const char *e = getenv("NS_GEMM_KPARTS"); e && *e) {
-        const int v = atoi(e);
-        if (v >= 1 && uint32_t(v) <= nb) p.kparts = uint32_t(v);
-    }
+    if (t.gemm_kparts >= 1 && uint32_t(t.gemm_kparts) <= nb) p.kparts = uint32_t(t.gemm_kparts);
     // one split-K part (padded to whole tiles) must stay under 4 GiB: 32-bit offsets in the kernel
     if (uint64_t(pair ? 2 : 1) * p.ntok * TT * p.ncol * rows_per_tile * 4 >= (uint64_t(1) << 32)) p.kparts = 1;
     return p;
@@ -461,18 +458,18 @@ RegPlan plan_reg(uint32_t cols, uint32_t rows, uint32_t batch, bool pair) {
 
 }  // namespace
 
-void gemm_reg_workspace_need(uint32_t cols, uint32_t rows, uint32_t batch, bool pair, size_t *part_floats,
-                             size_t *counters) {
-    const RegPlan p = plan_reg(cols, rows, batch, pair);
+void gemm_reg_workspace_need(uint32_t cols, uint32_t rows, uint32_t batch, bool pair, const Tuning &t,
+                             size_t *part_floats, size_t *counters) {
+    const RegPlan p = plan_reg(cols, rows, batch, pair, t);
     *part_floats = p.kparts > 1 ? size_t(p.kparts) * (pair ? 2 : 1) * (p.ntok * TT) * (p.ncol * (pair ? TC / 2 : TC)) : 0;
     *counters = size_t(p.ntok) * p.ncol;
 }
 
 hipError_t launch_gemm_reg(int acc, const uint8_t *w, const uint8_t *up, const uint16_t *x, const uint16_t *xsums,
                            void *out, uint32_t cols, uint32_t rows, uint32_t batch, float *partial,
-                           uint32_t *counters, hipStream_t stream) {
+                           uint32_t *counters, const Tuning &t, hipStream_t stream) {
     const bool pair = up != nullptr;
-    const RegPlan p = plan_reg(cols, rows, batch, pair);
+    const RegPlan p = plan_reg(cols, rows, batch, pair, t);
     const dim3 grid(p.ntok * p.ncol * p.kparts), block(kThreads);
     const uint32_t wbytes = rows * (cols / kQK) * kQ4Bytes;
     if (pair) {

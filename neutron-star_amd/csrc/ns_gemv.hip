@@ -979,11 +979,6 @@ __global__ __launch_bounds__(max_wg_waves_mt(TYPE, PAIR, NT) * 64) void gemv_mt_
     }
 }
 
-int env_int(const char *name, int dflt) {
-    const char *v = getenv(name);
-    return v && *v ? atoi(v) : dflt;
-}
-
 template <int TYPE, int LAYOUT, bool PAIR, bool PF>
 constexpr auto kernel_of() {
     return &gemv_kernel<TYPE, LAYOUT, PAIR, PF, 0>;
@@ -1035,15 +1030,15 @@ struct GemvPlan {
 // lm-head (4096 slabs, 2048 resident waves): one slab per workgroup 122.9 us;
 // one slab per wave (4096 waves) 125.1 us; the resident grid (two slabs per
 // wave) 127.2 us; 12288 waves (slabs cut between workgroups) 130.6 us.
-// NS_GEMV_WAVES sets the flattened grid's wave count instead.
+// Tuning::gemv_waves sets the flattened grid's wave count instead.
 GemvPlan plan_gemv(uint32_t cols, uint32_t rows, int resident_waves, uint32_t max_waves, uint32_t cus,
-                   bool slab_per_wg) {
+                   bool slab_per_wg, const Tuning &t) {
     GemvPlan p;
     const uint32_t nb = cols / kQK;
     p.nslabs = (rows + kRowTile - 1) / kRowTile;
     const uint32_t U = p.nslabs * nb;
     uint32_t cap = uint32_t(resident_waves > 0 ? resident_waves : 2048);
-    const int forced = env_int("NS_GEMV_WAVES", 0);
+    const int forced = t.gemv_waves;
     if (forced > 0) cap = uint32_t(forced);
     if (slab_per_wg && forced <= 0 && p.nslabs >= 2 * ((cap + kWgWaves - 1) / kWgWaves)) {
         p.W = kWgWaves < nb ? kWgWaves : nb;
@@ -1053,7 +1048,7 @@ GemvPlan plan_gemv(uint32_t cols, uint32_t rows, int resident_waves, uint32_t ma
     // About one slab per CU (the 15360-row gate/up projections: 240 slabs): one
     // workgroup per slab, as many waves as the CU holds -- nothing crosses
     // workgroups.  Otherwise the flattened split over resident 4-wave workgroups.
-    const bool whole = env_int("NS_GEMV_WHOLE", 1) != 0 && 4 * p.nslabs >= 3 * cus && p.nslabs <= 2 * cus;
+    const bool whole = t.gemv_whole != 0 && 4 * p.nslabs >= 3 * cus && p.nslabs <= 2 * cus;
     if (whole) {
         p.W = max_waves < nb ? max_waves : nb;
         p.G = p.nslabs;
@@ -1079,7 +1074,7 @@ int resident_waves(int layout) {
 // up) workgroups per slab when nb splits evenly and those fit one per CU (the
 // 3840 x 15360 down projection: 14.5 -> 14.2 us on MI355X against 15 workgroups
 // of 4 waves per slab); else the flattened split over 4-wave workgroups.
-GemvPlan plan_one_unit(uint32_t cols, uint32_t rows, uint32_t cus, uint32_t cu_waves) {
+GemvPlan plan_one_unit(uint32_t cols, uint32_t rows, uint32_t cus, uint32_t cu_waves, const Tuning &t) {
     GemvPlan p;
     const uint32_t nb = cols / kQK;
     p.nslabs = (rows + kRowTile - 1) / kRowTile;
@@ -1087,7 +1082,7 @@ GemvPlan plan_one_unit(uint32_t cols, uint32_t rows, uint32_t cus, uint32_t cu_w
     if (nb <= 16 && nb <= cu_waves && p.nslabs <= cus) {
         p.W = nb;
         p.G = p.nslabs;
-    } else if (env_int("NS_GEMV_QSLAB", 1) != 0 && nb % k == 0 && nb / k <= cu_waves && p.nslabs * k <= cus) {
+    } else if (t.gemv_qslab != 0 && nb % k == 0 && nb / k <= cu_waves && p.nslabs * k <= cus) {
         // k workgroups of nb/k waves per slab (the 60-block down projection: 4 x 15):
         // 4 parts cross workgroups instead of 15
         p.W = nb / k;
@@ -1109,23 +1104,23 @@ struct GemvChoice {
 // instance without the prefetch buffer (the gate/up pair and the down
 // projection: 3,600 units), that instance runs with one unit per wave: every
 // load is issued at launch and each wave computes as soon as its own unit
-// arrives.  NS_GEMV_PF=0/1 forces either instance.
+// arrives.  Tuning::gemv_pf = 0 / 1 forces either instance.
 template <int TYPE, bool PAIR>
-GemvChoice choose_gemv(int layout, uint32_t cols, uint32_t rows) {
+GemvChoice choose_gemv(int layout, uint32_t cols, uint32_t rows, const Tuning &t) {
     const uint32_t cus = uint32_t(device_shape().cus);
     const uint32_t nb = cols / kQK, units = ((rows + kRowTile - 1) / kRowTile) * nb;
-    const int force = env_int("NS_GEMV_PF", -1);
+    const int force = t.gemv_pf;
     const bool one = force == 0 || (force < 0 && int(units) <= resident_waves<TYPE, PAIR, false>(layout));
-    if (one) return {plan_one_unit(cols, rows, cus, uint32_t(resident_waves<TYPE, PAIR, false>(layout)) / cus), false};
+    if (one) return {plan_one_unit(cols, rows, cus, uint32_t(resident_waves<TYPE, PAIR, false>(layout)) / cus, t), false};
     return {plan_gemv(cols, rows, resident_waves<TYPE, PAIR, true>(layout), max_wg_waves(TYPE, PAIR, true), cus,
-                      !PAIR),
+                      !PAIR, t),
             true};
 }
 
-GemvChoice choose_gemv_for(int type, int layout, bool pair, uint32_t cols, uint32_t rows) {
-    if (pair) return choose_gemv<Q4_K, true>(layout, cols, rows);
-    if (type == Q4_K) return choose_gemv<Q4_K, false>(layout, cols, rows);
-    return choose_gemv<Q6_K, false>(layout, cols, rows);
+GemvChoice choose_gemv_for(int type, int layout, bool pair, uint32_t cols, uint32_t rows, const Tuning &t) {
+    if (pair) return choose_gemv<Q4_K, true>(layout, cols, rows, t);
+    if (type == Q4_K) return choose_gemv<Q4_K, false>(layout, cols, rows, t);
+    return choose_gemv<Q6_K, false>(layout, cols, rows, t);
 }
 
 template <int TYPE, int LAYOUT, bool PAIR, bool PF>
@@ -1165,7 +1160,7 @@ template <int TYPE, bool PAIR>
 hipError_t launch_typed(int layout, const uint8_t *w, const uint8_t *up, const float *x, float *out,
                         uint32_t cols, uint32_t rows, const Workspace &ws, hipStream_t stream,
                         const NormPrologue *np) {
-    const GemvChoice c = choose_gemv<TYPE, PAIR>(layout, cols, rows);
+    const GemvChoice c = choose_gemv<TYPE, PAIR>(layout, cols, rows, ws.tune);
     if (c.pf) launch_instance<TYPE, PAIR, true>(layout, c.plan, w, up, x, out, cols, rows, ws, stream, np);
     else launch_instance<TYPE, PAIR, false>(layout, c.plan, w, up, x, out, cols, rows, ws, stream, np);
     return hipGetLastError();
@@ -1175,7 +1170,7 @@ hipError_t launch_typed(int layout, const uint8_t *w, const uint8_t *up, const f
 template <int TYPE, int LAYOUT, bool PAIR, int NT, bool XH>
 struct Mt {
     static constexpr auto kernel() { return &gemv_mt_kernel<TYPE, LAYOUT, PAIR, NT, XH, PAIR>; }
-    static GemvPlan plan(uint32_t cols, uint32_t rows) {
+    static GemvPlan plan(uint32_t cols, uint32_t rows, const Tuning &t) {
         static int cache[64] = {};  // resident waves per CU, per device
         int dev = 0;
         (void)hipGetDevice(&dev);
@@ -1187,7 +1182,7 @@ struct Mt {
             w = wgs * kWgWaves;
         }
         const uint32_t cus = uint32_t(device_shape().cus);
-        return plan_gemv(cols, rows, w * int(cus), max_wg_waves_mt(TYPE, PAIR, NT), cus, false);
+        return plan_gemv(cols, rows, w * int(cus), max_wg_waves_mt(TYPE, PAIR, NT), cus, false, t);
     }
 };
 
@@ -1219,9 +1214,9 @@ uint32_t mt_tokens(uint32_t batch, bool xh) { return xh && batch <= 2 ? 2u : 4u;
 
 }  // namespace
 
-void gemv_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, bool pair, size_t *partial_floats,
-                         size_t *counters) {
-    const GemvPlan p = choose_gemv_for(type, layout, pair, cols, rows).plan;
+void gemv_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, bool pair, const Tuning &t,
+                         size_t *partial_floats, size_t *counters) {
+    const GemvPlan p = choose_gemv_for(type, layout, pair, cols, rows, t).plan;
     *partial_floats = size_t(p.G) * 2 * 64 * (pair ? 2 : 1);
     *counters = p.nslabs;
 }
@@ -1236,9 +1231,9 @@ hipError_t launch_gemv(int type, int layout, const uint8_t *w, const uint8_t *up
 }
 
 void gemv_mt_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, bool pair, uint32_t batch, bool xh,
-                            size_t *partial_floats, size_t *counters) {
+                            const Tuning &t, size_t *partial_floats, size_t *counters) {
     const uint32_t nt = mt_tokens(batch, xh);
-    const GemvPlan p = dispatch_mt(type, layout, pair, nt, xh, [&](auto m) { return decltype(m)::plan(cols, rows); });
+    const GemvPlan p = dispatch_mt(type, layout, pair, nt, xh, [&](auto m) { return decltype(m)::plan(cols, rows, t); });
     *partial_floats = size_t(p.G) * 2 * 64 * (pair ? 2 : 1) * nt;
     *counters = p.nslabs;
 }
@@ -1249,7 +1244,7 @@ hipError_t launch_gemv_mt(int type, int layout, const uint8_t *w, const uint8_t 
     const bool pair = up != nullptr;
     return dispatch_mt(type, layout, pair, mt_tokens(batch, xh), xh, [&](auto m) {
         using M = decltype(m);
-        const GemvPlan p = M::plan(cols, rows);
+        const GemvPlan p = M::plan(cols, rows, ws.tune);
         M::kernel()<<<dim3(p.G), dim3(p.W * 64), 0, stream>>>(w, up, x, batch, out, rows, cols / kQK, p.nslabs,
                                                                ws.partial, ws.counters);
         return hipGetLastError();

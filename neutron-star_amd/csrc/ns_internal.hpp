@@ -12,14 +12,27 @@ namespace ns {
 // Thread-local error text behind ns_last_error().
 void set_error(const std::string &msg);
 
+// Kernel-selection overrides of one context (ns_ctx_set_tuning), for tests and
+// experiments; the defaults select the measured plans.  Nothing reads the
+// environment: an engine process behaves the same whatever it inherits.
+struct Tuning {
+    int gemv_pf = -1;     // -1: plan; 0 / 1: force the one-unit / the prefetching decode GEMV
+    int gemv_waves = 0;   // > 0: the prefetching GEMV's flattened grid with this many waves
+    int gemv_whole = 1;   // 0: no whole-slab grid
+    int gemv_qslab = 1;   // 0: no k-workgroups-per-slab grid
+    int gemm_kparts = 0;  // > 0: the prefill GEMM's split-K parts
+    int gemm_q4_reg = 1;  // 0: the LDS-tile Q4_K GEMM instead of the register-fragment one
+};
+
 // Workspace owned by ns_ctx: fp32 partial sums and per-slab arrival counters
-// for reductions that span workgroups.  Counters are zero between calls (the
-// last workgroup of a slab resets its counter).
+// for reductions that span workgroups, and the context's tuning.  Counters are
+// zero between calls (the last workgroup of a slab resets its counter).
 struct Workspace {
     float *partial = nullptr;
     size_t partial_floats = 0;
     uint32_t *counters = nullptr;
     size_t counter_count = 0;
+    Tuning tune;
 };
 
 // The RMSNorm ahead of the FFN (rms: metal:510-511, mm:563), applied by a
@@ -39,8 +52,8 @@ hipError_t launch_gemv(int type, int layout, const uint8_t *w, const uint8_t *up
                        const Workspace &ws, hipStream_t stream, const NormPrologue *np = nullptr);
 
 // Required workspace for launch_gemv with these shapes.
-void gemv_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, bool pair, size_t *partial_floats,
-                         size_t *counters);
+void gemv_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, bool pair, const Tuning &t,
+                         size_t *partial_floats, size_t *counters);
 
 // Batch 2-4 (the reference's mm_fast / gate_up_geglu_mm regime): the weights
 // are streamed once for all tokens.  x: [batch][cols], fp16 (xh) or fp32;
@@ -49,20 +62,28 @@ hipError_t launch_gemv_mt(int type, int layout, const uint8_t *w, const uint8_t 
                           uint32_t batch, void *out, uint32_t cols, uint32_t rows, const Workspace &ws,
                           hipStream_t stream);
 void gemv_mt_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, bool pair, uint32_t batch, bool xh,
-                            size_t *partial_floats, size_t *counters);
+                            const Tuning &t, size_t *partial_floats, size_t *counters);
 
 // Workspace the prefill GEMM needs: Q4_K group sums of x, split-K parts, tile counters.
 void gemm_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, uint32_t batch, bool pair,
-                         size_t *floats, size_t *counters);
+                         const Tuning &t, size_t *floats, size_t *counters);
 
 // The Q4_K CDNA4 prefill GEMM with register-resident weight fragments
 // (ns_gemm_reg.hip): split-K parts it needs, and the launch.  xsums: the two
 // fp16 planes of x group sums; partial: the split-K parts.
-void gemm_reg_workspace_need(uint32_t cols, uint32_t rows, uint32_t batch, bool pair, size_t *part_floats,
-                             size_t *counters);
+void gemm_reg_workspace_need(uint32_t cols, uint32_t rows, uint32_t batch, bool pair, const Tuning &t,
+                             size_t *part_floats, size_t *counters);
 hipError_t launch_gemm_reg(int acc, const uint8_t *w, const uint8_t *up, const uint16_t *x, const uint16_t *xsums,
                            void *out, uint32_t cols, uint32_t rows, uint32_t batch, float *partial,
-                           uint32_t *counters, hipStream_t stream);
+                           uint32_t *counters, const Tuning &t, hipStream_t stream);
+
+// The FP16-mode prefill GEMM on the CDNA4 layout (ns_gemm_f16.hip): fp16 weight
+// tiles with per-row power-of-two scales (ns_tile16.hpp), no x group sums.
+void gemm_f16_workspace_need(uint32_t cols, uint32_t rows, uint32_t batch, bool pair, const Tuning &t,
+                             size_t *part_floats, size_t *counters);
+hipError_t launch_gemm_f16(int type, const uint8_t *w, const uint8_t *up, const uint16_t *x, void *out, uint32_t cols,
+                           uint32_t rows, uint32_t batch, float *partial, uint32_t *counters, const Tuning &t,
+                           hipStream_t stream);
 
 // Prefill GEMM over fp16 x [batch][cols]: plain (fp32 out [batch][rows]) or the
 // gate/up pair with GeGLU (fp16 h [batch][rows]).

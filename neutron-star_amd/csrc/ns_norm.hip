@@ -32,8 +32,8 @@ __device__ __forceinline__ float block_sum(float s, float *part) {
 // workgroup per row; each thread owns the elements k = tid + j*256.  The second
 // pass re-reads y where this thread stored it, as the reference does.
 template <bool HY, bool ADD, bool THEN, bool HN>
-__global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *__restrict__ x, const float *__restrict__ w,
-                                                         const float *__restrict__ residual,
+__global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *x, const float *__restrict__ w,
+                                                         const float *residual,
                                                          const float *__restrict__ scale,
                                                          const float *__restrict__ next_w, uint32_t width, float eps,
                                                          void *y, void *__restrict__ next) {
@@ -70,11 +70,13 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *__restri
 // The same family with the row held in registers (ns::rms_row): one memory round
 // trip per row.  HY: fp16 y (rms_half, no residual); HZ: fp16 next.
 template <bool HY, bool HZ>
-__global__ __launch_bounds__(1024) void rmsnorm_vec_kernel(const float *__restrict__ x, const float *__restrict__ w,
-                                                          const float *__restrict__ residual,
+// x, residual and y are not restrict: an fp32 y may alias x or residual (every
+// thread loads its whole row share before it stores).
+__global__ __launch_bounds__(1024) void rmsnorm_vec_kernel(const float *x, const float *__restrict__ w,
+                                                          const float *residual,
                                                           const float *__restrict__ scale,
                                                           const float *__restrict__ next_w, uint32_t width, float eps,
-                                                          void *__restrict__ y, void *__restrict__ next) {
+                                                          void *y, void *__restrict__ next) {
     __shared__ float part[16];
     typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
     const size_t base4 = size_t(blockIdx.x) * (width / 4);

@@ -70,9 +70,13 @@ __device__ __forceinline__ Q6Quarters q6_quarters(uint32_t a, uint32_t b, uint32
     return q;
 }
 
-// GeGLU (metal/gemma4.metal:78).
+// GeGLU (metal/gemma4.metal:78): 0.5*g*(1 + tanh(z)), z = 0.7978845608028654*g*(1 + 0.044715*g*g).
+// Evaluated through the identity 0.5*(1 + tanh(z)) = 1/(1 + exp(-2z)) as g / (1 + 2^(-2z*log2(e))):
+// one exp2 and one reciprocal, no cancellation for negative g, and exact limits (g for
+// large g, -0 for very negative g).  Within a few fp32 ulps of the tanh form.
 __device__ __forceinline__ float gelu_tanh(float g) {
-    return 0.5f * g * (1.0f + tanhf(0.7978845608028654f * g * (1.0f + 0.044715f * g * g)));
+    const float z = 0.7978845608028654f * g * (1.0f + 0.044715f * g * g);
+    return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z * -2.8853900817779268f));
 }
 
 }  // namespace ns

@@ -53,8 +53,8 @@ struct RmsRow {
 };
 
 template <int KV>
-__device__ __forceinline__ void rms_row_load(RmsRow<KV> &rr, const float4 *__restrict__ x,
-                                             const float4 *__restrict__ w, const float4 *__restrict__ res,
+__device__ __forceinline__ void rms_row_load(RmsRow<KV> &rr, const float4 *x,
+                                             const float4 *__restrict__ w, const float4 *res,
                                              const float *__restrict__ scale, const float4 *__restrict__ next_w,
                                              uint32_t n4) {
     const uint32_t nt = blockDim.x, tid = threadIdx.x;
@@ -104,8 +104,8 @@ __device__ __forceinline__ void rms_row_finish(RmsRow<KV> &rr, bool has_res, boo
 }
 
 template <int KV, class OutY, class OutZ>
-__device__ __forceinline__ void rms_row(const float4 *__restrict__ x, const float4 *__restrict__ w,
-                                        const float4 *__restrict__ res, const float *__restrict__ scale,
+__device__ __forceinline__ void rms_row(const float4 *x, const float4 *__restrict__ w,
+                                        const float4 *res, const float *__restrict__ scale,
                                         const float4 *__restrict__ next_w, uint32_t n4, float eps, float *part,
                                         OutY &&out_y, OutZ &&out_z) {
     RmsRow<KV> rr;

@@ -153,9 +153,13 @@ public:
     void ffn_block(hipStream_t e, const Tensor &gate, const Tensor &up, const Tensor &down, const void *in, void *mid,
                    float *out, uint32_t batch, bool prefill, bool swa, bool exact_ffn) const {
         const bool fast_swa = prefill && swa && !exact_ffn;
-        if (prefill) {
+        if (prefill && batch > 4) {
             gate_up_geglu_rm32(e, gate, up, static_cast<const uint16_t *>(in), static_cast<uint16_t *>(mid), batch,
                                fast_swa);
+        } else if (prefill) {
+            // mm:569: a prefill of 2-4 tokens (MTP verification) takes gate_up_geglu, the
+            // small-batch kernel, in FP32 accumulation whatever the layer's mode
+            gate_up_geglu(e, gate, up, static_cast<const uint16_t *>(in), static_cast<uint16_t *>(mid), batch);
         } else {
             // mm:570-571: the fused decode kernel; batches of fp32 tokens take it token by token
             const uint32_t c = cols(gate), r = rows(gate);

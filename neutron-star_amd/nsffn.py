@@ -63,6 +63,8 @@ def lib():
             "ns_abi_version": [],
             "ns_ctx_create": [i32, ctypes.POINTER(vp)],
             "ns_ctx_destroy": [vp],
+            "ns_ctx_workspace_bytes": [vp, ctypes.POINTER(u64)],
+            "ns_ctx_set_tuning": [vp, ctypes.c_char_p, i32],
             "ns_matmul": [vp, vp, i32, i32, u32, u32, u32, vp, i32, vp, vp],
             "ns_gate_up_geglu_decode": [vp, vp, vp, i32, u32, u32, vp, vp, vp],
             "ns_gate_up_geglu_rm32": [vp, vp, vp, i32, u32, u32, u32, vp, vp, i32, vp],
@@ -112,11 +114,20 @@ def check(rc):
 
 
 def _ptr(a):
+    """Device pointer of a torch CUDA tensor (None passes through).  Host arrays are
+    refused: a host pointer handed to a kernel faults the GPU."""
     if a is None:
         return None
-    if isinstance(a, np.ndarray):
-        return a.ctypes.data
+    if isinstance(a, np.ndarray) or not getattr(a, "is_cuda", False):
+        raise TypeError("device entry points take torch CUDA tensors, got " + type(a).__name__)
     return a.data_ptr()
+
+
+def _hptr(a):
+    """Host pointer of a numpy array for the host-side utilities."""
+    if not isinstance(a, np.ndarray):
+        raise TypeError("host utilities take numpy arrays, got " + type(a).__name__)
+    return a.ctypes.data
 
 
 def _stream(stream):
@@ -134,7 +145,7 @@ def default_threads():
 
 def synth_blocks(qtype, seed, nblocks, first=0, nthreads=None):
     out = np.empty(nblocks * BLOCK_BYTES[qtype], dtype=np.uint8)
-    check(lib().ns_synth_blocks(qtype, seed, first, nblocks, _ptr(out), nthreads or default_threads()))
+    check(lib().ns_synth_blocks(qtype, seed, first, nblocks, _hptr(out), nthreads or default_threads()))
     return out
 
 
@@ -145,13 +156,13 @@ def synth_weights(qtype, seed, rows, cols, nthreads=None):
 
 def synth_normal_f32(seed, n, first=0, nthreads=None):
     out = np.empty(n, dtype=np.float32)
-    check(lib().ns_synth_normal_f32(seed, first, n, _ptr(out), nthreads or default_threads()))
+    check(lib().ns_synth_normal_f32(seed, first, n, _hptr(out), nthreads or default_threads()))
     return out
 
 
 def synth_normal_f16(seed, n, first=0, nthreads=None):
     out = np.empty(n, dtype=np.uint16)
-    check(lib().ns_synth_normal_f16(seed, first, n, _ptr(out), nthreads or default_threads()))
+    check(lib().ns_synth_normal_f16(seed, first, n, _hptr(out), nthreads or default_threads()))
     return out
 
 
@@ -162,7 +173,7 @@ def layer_seed(seed, layer):
 def retile(src, qtype, cols, rows, from_layout, to_layout):
     src = np.ascontiguousarray(src, dtype=np.uint8)
     dst = np.empty_like(src)
-    check(lib().ns_retile(_ptr(src), _ptr(dst), qtype, cols, rows, from_layout, to_layout))
+    check(lib().ns_retile(_hptr(src), _hptr(dst), qtype, cols, rows, from_layout, to_layout))
     return dst
 
 
@@ -180,17 +191,17 @@ def tensor_table(rows):
 
 def nsmffn_fingerprint(head, gguf_size):
     head = np.ascontiguousarray(head, dtype=np.uint8)
-    return lib().ns_nsmffn_fingerprint(_ptr(head), head.size, gguf_size)
+    return lib().ns_nsmffn_fingerprint(_hptr(head), head.size, gguf_size)
 
 
 def nsmffn_convert(path, gguf, data_offset, table):
     gguf = np.ascontiguousarray(gguf, dtype=np.uint8)
-    check(lib().ns_nsmffn_convert(str(path).encode(), _ptr(gguf), gguf.size, data_offset, _ptr(table), len(table)))
+    check(lib().ns_nsmffn_convert(str(path).encode(), _hptr(gguf), gguf.size, data_offset, _hptr(table), len(table)))
 
 
 def nsmffn_convert_in_place(model_path, metadata_path, data_offset, table):
     check(lib().ns_nsmffn_convert_in_place(str(model_path).encode(), str(metadata_path).encode(), data_offset,
-                                           _ptr(table), len(table)))
+                                           _hptr(table), len(table)))
 
 
 class NsmffnFile:
@@ -200,7 +211,7 @@ class NsmffnFile:
 
     def __init__(self, path, gguf_size, fingerprint, table):
         h = ctypes.c_void_p()
-        check(lib().ns_nsmffn_open(str(path).encode(), gguf_size, fingerprint, _ptr(table), len(table),
+        check(lib().ns_nsmffn_open(str(path).encode(), gguf_size, fingerprint, _hptr(table), len(table),
                                    ctypes.byref(h)))
         self.handle = h
 
@@ -310,7 +321,7 @@ class GgufFile:
         n = ctypes.c_uint32()
         check(lib().ns_gguf_ffn_table(self.handle, None, 0, ctypes.byref(n)))
         table = np.zeros(n.value, dtype=TENSOR_DESC)
-        check(lib().ns_gguf_ffn_table(self.handle, _ptr(table), n.value, ctypes.byref(n)))
+        check(lib().ns_gguf_ffn_table(self.handle, _hptr(table), n.value, ctypes.byref(n)))
         return table
 
     def bytes_at(self, offset, nbytes):
@@ -330,6 +341,17 @@ class Context:
         if self.handle:
             lib().ns_ctx_destroy(self.handle)
             self.handle = None
+
+    def set_tuning(self, key, value):
+        """Test hook: override one kernel-selection choice of this context
+        (ns_ctx_set_tuning; keys gemv_pf, gemv_waves, gemv_whole, gemv_qslab,
+        gemm_kparts, gemm_q4_reg)."""
+        check(lib().ns_ctx_set_tuning(self.handle, key.encode(), int(value)))
+
+    def workspace_bytes(self):
+        n = ctypes.c_uint64()
+        check(lib().ns_ctx_workspace_bytes(self.handle, ctypes.byref(n)))
+        return n.value
 
     def __del__(self):
         try:
@@ -364,8 +386,10 @@ class Context:
         GeGLU into `mid`, then down into `out`, in the mode fast_swa_ffn = prefill && swa &&
         !exact_ffn (mm:565).  Prefill: inp/mid fp16 bits; decode: fp32."""
         fast = bool(prefill and swa and not exact_ffn)
-        if prefill:
+        if prefill and batch > 4:
             self.gate_up_geglu_rm32(gate, up, layout, cols, ffn, batch, inp, mid, fast, stream)
+        elif prefill:  # mm:569: 2-4 tokens take gate_up_geglu (small-batch kernel, FP32)
+            self.gate_up_geglu(gate, up, layout, cols, ffn, batch, inp, mid, stream)
         else:
             for t in range(batch):
                 self.gate_up_geglu_decode(gate, up, layout, cols, ffn, inp[t * cols:(t + 1) * cols] if batch > 1

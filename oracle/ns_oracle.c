@@ -125,6 +125,110 @@ static int check(int type, int layout, uint64_t cols, uint64_t rows) {
     return 0;
 }
 
+/* ---- FP16-mode tiles -------------------------------------------------------
+ * The FP16 mode multiplies fp16 tiles of the weights, the reference's
+ * half(d*sc*q - dmin*m) / half(d*sc*(v-32)) (metal/gemma4.metal:229-232, :415-419),
+ * with a per-row power of two c folded in so that the tile is one packed fp16 FMA
+ * from the quant bits (this build's kernels, neutron-star_amd/csrc/ns_tile16.hpp):
+ *   M = max over the row's blocks of max(|d|, |dmin|) (Q6_K: |d|)
+ *   c = 2^(-15 - ceil(log2 M)), c = 1 when M == 0
+ *   A = RNE16(d*sc*2^24*c),  B = RNE16(-dmin*m*c)  (Q6_K: B = RNE16(-32*d*sc*c))
+ *   F = RNE16(q*2^-24*A + B)                       (Q6_K: q is the 6-bit v)
+ * and the output is RNE11((sum_k F*x) / c).  Every quantity before RNE16 is exact
+ * in double, so each RNE16 here is one rounding of the exact value, as the fused
+ * fp16 FMA and the fp32 -> fp16 conversions of the kernel are. */
+
+/* Round an exact double to binary16, nearest even, subnormals kept, overflow to inf;
+ * returned as the (exact) double of the fp16 value. */
+static double rne16(double v) {
+    const double a = fabs(v);
+    if (a == 0.0) return v;
+    int ex;
+    frexp(a, &ex);                       /* a = m * 2^ex, m in [0.5, 1) */
+    int e = ex - 1;                      /* a in [2^e, 2^(e+1)) */
+    if (e < -14) e = -14;                /* subnormal range: ulp 2^-24 */
+    const double ulp = ldexp(1.0, e - 10);
+    double q = nearbyint(a / ulp);       /* the default mode rounds to nearest even */
+    double r = q * ulp;
+    if (r > 65504.0) r = INFINITY;
+    return v < 0 ? -r : r;
+}
+
+static void row_scale(int type, int layout, const uint8_t *w, uint64_t cols, uint64_t row, double *c24,
+                      double *inv_c) {
+    const uint64_t nb = cols / 256;
+    const size_t bs = block_bytes(type);
+    double M = 0.0;
+    for (uint64_t b = 0; b < nb; ++b) {
+        const uint8_t *blk = w + nso_block_index(layout, row, b, nb) * bs;
+        if (type == NSO_Q4_K) {
+            M = fmax(M, fabs((double)rd_f16(blk)));
+            M = fmax(M, fabs((double)rd_f16(blk + 2)));
+        } else {
+            M = fmax(M, fabs((double)rd_f16(blk + 208)));
+        }
+    }
+    if (!(M > 0.0)) {
+        *c24 = 16777216.0;
+        *inv_c = 1.0;
+        return;
+    }
+    int ex;
+    const double m = frexp(M, &ex);      /* M = m * 2^ex */
+    const int e = m == 0.5 ? ex - 1 : ex; /* ceil(log2 M) */
+    *c24 = ldexp(1.0, 9 - e);
+    *inv_c = ldexp(1.0, 15 + e);
+}
+
+/* F of element i of a block, given the row's c24 = c * 2^24. */
+static double f16_tile_value(int type, const uint8_t *b, uint32_t i, double c24) {
+    const double c = c24 * 5.9604644775390625e-08;
+    if (type == NSO_Q4_K) {
+        const double d = rd_f16(b), dm = rd_f16(b + 2);
+        const uint8_t *s = b + 4, *q = b + 16;
+        const uint32_t g = i / 32, l = i % 32;
+        uint8_t sc, m;
+        if (g < 4) {
+            sc = s[g] & 63;
+            m = s[g + 4] & 63;
+        } else {
+            sc = (uint8_t)((s[g + 4] & 15) | ((s[g - 4] >> 6) << 4));
+            m = (uint8_t)((s[g + 4] >> 4) | ((s[g] >> 6) << 4));
+        }
+        const uint8_t v = (g & 1) ? (uint8_t)(q[(g / 2) * 32 + l] >> 4) : (uint8_t)(q[(g / 2) * 32 + l] & 15);
+        const double A = rne16(d * sc * c24), B = rne16(-dm * m * c);
+        return rne16((double)v * 5.9604644775390625e-08 * A + B);
+    }
+    const uint8_t *ql = b, *qh = b + 128;
+    const int8_t *scs = (const int8_t *)(b + 192);
+    const double d = rd_f16(b + 208);
+    const uint32_t half = i / 128, p = i % 128, l = p % 32, quarter = p / 32;
+    const uint8_t *lo = ql + half * 64, *hi = qh + half * 32;
+    int v;
+    if (quarter == 0) v = (lo[l] & 15) | (((hi[l] >> 0) & 3) << 4);
+    else if (quarter == 1) v = (lo[l + 32] & 15) | (((hi[l] >> 2) & 3) << 4);
+    else if (quarter == 2) v = (lo[l] >> 4) | (((hi[l] >> 4) & 3) << 4);
+    else v = (lo[l + 32] >> 4) | (((hi[l] >> 6) & 3) << 4);
+    const double sc = scs[half * 8 + (l / 16) + quarter * 2];
+    const double A = rne16(d * sc * c24), B = rne16(-32.0 * d * sc * c);
+    return rne16((double)v * 5.9604644775390625e-08 * A + B);
+}
+
+int nso_f16_tile_row(int type, int layout, const uint8_t *w, uint64_t cols, uint64_t rows, uint64_t row,
+                     float *tile, float *inv_c) {
+    if (check(type, layout, cols, rows) || row >= rows) return -1;
+    double c24, ic;
+    row_scale(type, layout, w, cols, row, &c24, &ic);
+    const uint64_t nb = cols / 256;
+    const size_t bs = block_bytes(type);
+    for (uint64_t b = 0; b < nb; ++b) {
+        const uint8_t *blk = w + nso_block_index(layout, row, b, nb) * bs;
+        for (uint32_t i = 0; i < 256; ++i) tile[b * 256 + i] = (float)f16_tile_value(type, blk, i, c24);
+    }
+    *inv_c = (float)ic;
+    return 0;
+}
+
 int nso_dequant_row(int type, int layout, const uint8_t *w, uint64_t cols, uint64_t rows,
                     uint64_t row, float *out) {
     if (check(type, layout, cols, rows) || row >= rows) return -1;
@@ -227,16 +331,19 @@ static void *gemm_worker(void *p) {
     float *row = (float *)malloc(j->cols * sizeof(float));
     float *acc = (float *)malloc(B * sizeof(float));
     for (uint64_t r = j->r0; r < j->r1; ++r) {
-        nso_dequant_row(j->type, j->layout, j->w, j->cols, j->rows, r, row);
+        float inv_c = 1.0f;
+        if (j->acc_mode == 1) nso_f16_tile_row(j->type, j->layout, j->w, j->cols, j->rows, r, row, &inv_c);
+        else nso_dequant_row(j->type, j->layout, j->w, j->cols, j->rows, r, row);
         for (uint64_t t = 0; t < B; ++t) acc[t] = 0;
         for (uint64_t k = 0; k < j->cols; ++k) {
             const float wk = row[k];
             const float *xk = j->xt + k * B;
             for (uint64_t t = 0; t < B; ++t) acc[t] += wk * xk[t];
-            if (j->acc_mode == 1 && (k % 256) == 255)
-                for (uint64_t t = 0; t < B; ++t) acc[t] = nso_round_f16p(acc[t]);
         }
-        for (uint64_t t = 0; t < B; ++t) j->out[t * j->rows + r] = acc[t];
+        /* FP16 mode: the sum of the scaled tiles, times 1/c (a power of two: exact),
+         * rounded once to fp16 precision (metal:394, :489 write a half tile) */
+        for (uint64_t t = 0; t < B; ++t)
+            j->out[t * j->rows + r] = j->acc_mode == 1 ? nso_round_f16p(acc[t] * inv_c) : acc[t];
     }
     free(acc);
     free(row);
@@ -295,8 +402,6 @@ int nso_gemm(int type, int layout, const uint8_t *w, uint64_t cols, uint64_t row
     j.rows = rows; j.batch = batch; j.xt = xt; j.out = out;
     run_rows(&j, rows, nthreads, gemm_worker);
     free(xt);
-    if (acc_mode == 1) /* FP16 mode: outputs carry fp16 precision (metal:394, :489 widen half) */
-        for (uint64_t i = 0; i < rows * batch; ++i) out[i] = nso_round_f16p(out[i]);
     return 0;
 }
 

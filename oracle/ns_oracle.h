@@ -21,9 +21,14 @@
  *   dot_row: oracle/_ref dot_row bit-exact, linearity and one-hot columns.
  *   gelu_tanh: closed forms (gelu(0)=0, large |g| -> relu, odd part identity).
  *   round_f16p: equals numpy float16 rounding over the fp16 normal range.
- *   FP16-accumulation mode (nso_gemm acc_mode=1): parity unpinned -- the
- *     reference's Apple simdgroup_half8x8 rounding cannot run here; it is
- *     checked only against the fp32 path within the 1e-2 tolerance.
+ *   FP16 mode (nso_f16_tile_row, nso_gemm acc_mode=1): the tile formula against
+ *     closed forms (power-of-two blocks whose tiles are exact, hand-computed
+ *     roundings of A, B and F, subnormal B, the row scale's ceil(log2 M) at and
+ *     just past powers of two, M = 0) and the output schedule against known
+ *     answers (integer sums 2049 -> 2048 in one block, 2049 + 1 over two blocks
+ *     -> 2050: one rounding at the end, none per block).  What stays unpinned is
+ *     the reference's own FP16 arithmetic on Apple simdgroup_half8x8 hardware,
+ *     which runs nowhere here; this mode is within 1e-2 of the FP32 path.
  */
 #ifndef NS_ORACLE_H
 #define NS_ORACLE_H
@@ -73,11 +78,18 @@ int nso_rmsnorm(const float *x, const float *w, const float *residual, const flo
 int nso_gate_up_geglu(int layout, const uint8_t *wg, const uint8_t *wu, uint64_t cols,
                       uint64_t rows, const float *x, float *h, int nthreads);
 
+/* FP16-mode tile of one row (cols values): F = RNE16(q*2^-24*A + B) with the row
+ * scale c folded into A and B (formulas in ns_oracle.c), and 1/c.  F*(1/c) is the
+ * reference's half(d*sc*q - dmin*m) / half(d*sc*(v-32)) up to the order of its
+ * roundings (metal:229-232, :415-419). */
+int nso_f16_tile_row(int type, int layout, const uint8_t *w, uint64_t cols, uint64_t rows, uint64_t row,
+                     float *tile, float *inv_c);
+
 /* Prefill contraction: out[t][r] = sum_k W[r][k] * x[t][k] for t < batch.
- * x is fp16 bits [batch][cols].  acc_mode 0 = FP32 (sequential fp32 sum, fp32 out);
- * acc_mode 1 = FP16 mode as defined by this build: the fp32 running sum is
- * rounded to fp16 precision (nso_round_f16p) at every 256-wide super-block
- * boundary, so the result carries fp16 precision (without fp16's overflow). */
+ * x is fp16 bits [batch][cols].  acc_mode 0 = FP32 (quant.cpp values, sequential
+ * fp32 sum, fp32 out); acc_mode 1 = FP16 mode: the tiles of nso_f16_tile_row,
+ * a sequential fp32 sum, times 1/c, rounded once to fp16 precision
+ * (nso_round_f16p: 11 significant bits, fp32 exponent range). */
 int nso_gemm(int type, int layout, const uint8_t *w, uint64_t cols, uint64_t rows,
              uint64_t batch, const uint16_t *x_f16, int acc_mode, float *out, int nthreads);
 

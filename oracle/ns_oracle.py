@@ -47,6 +47,7 @@ def lib():
         L.nso_gelu_tanh.restype = f32
         L.nso_gate_up_geglu.argtypes = [i32, vp, vp, u64, u64, vp, vp, i32]
         L.nso_gemm.argtypes = [i32, i32, vp, u64, u64, u64, vp, i32, vp, i32]
+        L.nso_f16_tile_row.argtypes = [i32, i32, vp, u64, u64, u64, vp, vp]
         L.nso_gate_up_geglu_prefill.argtypes = [i32, vp, vp, u64, u64, u64, vp, i32, vp, i32]
         L.nso_rmsnorm.argtypes = [vp, vp, vp, vp, vp, u64, u64, f32, vp, vp]
         _lib = L
@@ -99,6 +100,17 @@ def gate_up_geglu(layout, wg, wu, cols, rows, x, nthreads=None):
     h = np.empty(rows, dtype=np.float32)
     assert lib().nso_gate_up_geglu(layout, _p(wg), _p(wu), cols, rows, _p(x), _p(h), _nt(nthreads)) == 0
     return h
+
+
+def f16_tile_rows(qtype, layout, w, cols, rows, row0=0, nrows=None):
+    """FP16-mode tiles of rows [row0, row0+nrows): (tiles [nrows][cols], inv_c [nrows])."""
+    nrows = rows - row0 if nrows is None else nrows
+    out = np.empty((nrows, cols), dtype=np.float32)
+    inv = np.empty(nrows, dtype=np.float32)
+    for i in range(nrows):
+        rc = lib().nso_f16_tile_row(qtype, layout, _p(w), cols, rows, row0 + i, _p(out[i]), _p(inv[i:i + 1]))
+        assert rc == 0
+    return out, inv
 
 
 def gemm(qtype, layout, w, cols, rows, batch, x_f16, acc_mode, nthreads=None):

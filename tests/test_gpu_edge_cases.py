@@ -121,8 +121,8 @@ GEMM_KERNELS = [(N.Q4_K, "1"), (N.Q4_K, "0"), (N.Q6_K, "1")]
 @pytest.mark.parametrize("acc", [N.ACC_FP32, N.ACC_FP16], ids=["fp32acc", "fp16acc"])
 @pytest.mark.parametrize("layout", LAYOUTS, ids=LNAME.get)
 @pytest.mark.parametrize("qtype,reg", GEMM_KERNELS, ids=["q4k-reg", "q4k-lds", "q6k"])
-def test_special_blocks_gemm(ctx, monkeypatch, qtype, reg, layout, acc):
-    monkeypatch.setenv("NS_GEMM_Q4_REG", reg)
+def test_special_blocks_gemm(ctx, tune, qtype, reg, layout, acc):
+    tune("gemm_q4_reg", reg)
     rows, cols, batch = 128, 1024, 40
     host = special_matrix(qtype, rows, cols, 17 + qtype)
     w = laid(host, qtype, rows, cols, layout)

@@ -104,11 +104,11 @@ def weights(seed, rows, cols, layout):
 @pytest.mark.parametrize("force_pf", [None, "1"], ids=["auto", "prefetch"])
 @pytest.mark.parametrize("layout", [N.CDNA4, N.NSMFFN, N.ROW_MAJOR], ids=LNAME.get)
 @pytest.mark.parametrize("shape", [(768, 128), (3840, 15360)], ids=["small", "gemma"])
-def test_rms_gate_up_geglu_decode(ctx, layout, shape, force_pf, monkeypatch):
+def test_rms_gate_up_geglu_decode(ctx, layout, shape, force_pf, tune):
     """rms (mm:563) fused ahead of the pair GEMV.  The default grid (one super-block per wave,
     whole slabs) takes the barrier-free form; the prefetching instance the workgroup form."""
     if force_pf:
-        monkeypatch.setenv("NS_GEMV_PF", force_pf)
+        tune("gemv_pf", force_pf)
     cols, rows = shape
     if layout == N.ROW_MAJOR and rows == 128:
         rows = 136  # ragged last slab
@@ -142,10 +142,10 @@ def test_rms_fused_equals_rms_then_gate_up(ctx):
 @pytest.mark.parametrize("force_pf", ["0", "1"], ids=["one_unit", "prefetch"])
 @pytest.mark.parametrize("layout", [N.CDNA4, N.NSMFFN, N.ROW_MAJOR], ids=LNAME.get)
 @pytest.mark.parametrize("qtype", [N.Q4_K, N.Q6_K], ids=["q4k", "q6k"])
-def test_gemv_both_instances(ctx, qtype, layout, force_pf, monkeypatch):
+def test_gemv_both_instances(ctx, qtype, layout, force_pf, tune):
     """The decode GEMV with each kernel instance forced (NS_GEMV_PF), on shapes with more
     than 16 super-blocks per row, so slabs are cut between workgroups in both."""
-    monkeypatch.setenv("NS_GEMV_PF", force_pf)
+    tune("gemv_pf", force_pf)
     cols, rows = 5120, (200 if layout == N.ROW_MAJOR else 192)
     host = N.synth_weights(qtype, 61, rows, cols)
     w = dev(host if layout == N.ROW_MAJOR else N.retile(host, qtype, cols, rows, N.ROW_MAJOR, layout))

@@ -18,6 +18,14 @@ torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
 TOL32, TOL16 = 1e-3, 1e-2
+# FP16-mode outputs against the oracle's FP16 mode (the same tiles and one final rounding to
+# 11 bits): they differ only by the fp32 summation order before that rounding, i.e. at most
+# one fp16 rounding step of an output, 2^-11 < 1e-3 of the row's largest value.
+TOL16_SAME = 1e-3
+# The gate/up pair rounds g and u to 11 bits before GeGLU: a rounding step of g or u that
+# flips between the two summation orders is amplified by GeGLU (by up to ~6 near its minimum,
+# g ~ -2.5), plus h's own rounding; measured against the largest |h| of the columns compared.
+TOL16_SAME_PAIR = 5e-3
 LAYOUTS = [N.CDNA4, N.NSMFFN, N.ROW_MAJOR]
 LNAME = {N.CDNA4: "cdna4", N.NSMFFN: "nsmffn", N.ROW_MAJOR: "rowmajor"}
 
@@ -95,11 +103,11 @@ def test_gemv(ctx, qtype, cols, rows, name, layout):
 @pytest.mark.parametrize("qtype,rows,layout", [(N.Q6_K, 3840, N.CDNA4), (N.Q4_K, 3840, N.NSMFFN),
                                                (N.Q6_K, 3840 - 24, N.ROW_MAJOR)],
                          ids=["q6k_cdna4", "q4k_nsmffn", "q6k_rowmajor_ragged"])
-def test_down_plans(ctx, monkeypatch, qslab, qtype, rows, layout):
+def test_down_plans(ctx, tune, qslab, qtype, rows, layout):
     """The 60-block down projection under both grids of the one-unit instance:
     4 workgroups of 15 waves per slab (default) and the flattened split
     (NS_GEMV_QSLAB=0, 15 workgroups per slab); both meet the bar and repeat."""
-    monkeypatch.setenv("NS_GEMV_QSLAB", qslab)
+    tune("gemv_qslab", qslab)
     cols = 15360
     host, w = weights(qtype, 41, rows, cols, layout)
     x = f32(cols, 42)
@@ -148,9 +156,9 @@ def _run(ctx, qtype, w, layout, cols, rows, x):
 
 
 @pytest.mark.parametrize("waves", [None, "2048", "12288"], ids=["slab_per_wg", "resident", "cut_slabs"])
-def test_stream_grids(ctx, monkeypatch, waves):
+def test_stream_grids(ctx, tune, waves):
     if waves:
-        monkeypatch.setenv("NS_GEMV_WAVES", waves)
+        tune("gemv_waves", waves)
     host, w, x, cols, rows = _lm_head(ctx, N.CDNA4)
     ref = O.gemv(N.Q6_K, O.ROW_MAJOR, host, cols, rows, x)
     y = _run(ctx, N.Q6_K, w, N.CDNA4, cols, rows, x)
@@ -181,18 +189,18 @@ STREAM_CASES = [
 
 
 @pytest.mark.parametrize("qtype,cols,rows,layout,name", STREAM_CASES, ids=[c[4] for c in STREAM_CASES])
-def test_stream_shapes(ctx, monkeypatch, qtype, cols, rows, layout, name):
+def test_stream_shapes(ctx, tune, qtype, cols, rows, layout, name):
     """The streaming instance forced (NS_GEMV_PF=1) on shapes from one slab to a
     ragged row-major lm-head, with fewer super-blocks per slab than waves."""
-    monkeypatch.setenv("NS_GEMV_PF", "1")
+    tune("gemv_pf", "1")
     host, w = weights(qtype, 31, rows, cols, layout)
     x = f32(cols, 32)
     ref = O.gemv(qtype, O.ROW_MAJOR, host, cols, rows, x)
     assert rel_err(_run(ctx, qtype, w, layout, cols, rows, x), ref) <= TOL32
 
 
-def test_stream_gate_up_pair(ctx, monkeypatch):
-    monkeypatch.setenv("NS_GEMV_PF", "1")
+def test_stream_gate_up_pair(ctx, tune):
+    tune("gemv_pf", "1")
     cols, rows = 3840, 15360
     hg, wg = weights(N.Q4_K, 21, rows, cols, N.CDNA4)
     hu, wu = weights(N.Q4_K, 22, rows, cols, N.CDNA4)
@@ -274,7 +282,7 @@ def test_prefill_gate_up_small(ctx, cols, rows, batch, acc, layout):
     assert rel_err(got, ref32) <= (TOL32 if acc == N.ACC_FP32 else TOL16)
     if acc == N.ACC_FP16:
         ref16 = O.gate_up_geglu_prefill(O.ROW_MAJOR, hg, hu, cols, rows, batch, x, 1)
-        assert rel_err(got, ref16) <= 4e-3
+        assert rel_err(got, ref16) <= TOL16_SAME_PAIR
 
 
 @pytest.mark.parametrize("layout", [N.CDNA4, N.NSMFFN], ids=LNAME.get)
@@ -298,7 +306,7 @@ def test_prefill_down_small(ctx, cols, rows, batch, qtype, acc, layout):
     if acc == N.ACC_FP16:
         assert not np.any(got.view(np.uint32) & 0x1FFF)  # fp16 precision: 11 significant bits
         ref16 = O.gemm(qtype, O.ROW_MAJOR, hw, cols, rows, batch, x, 1)
-        assert rel_err(got, ref16) <= 4e-3
+        assert rel_err(got, ref16) <= TOL16_SAME
 
 
 # Forced split-K: every part count path of both Q4_K kernels (register-fragment,
@@ -310,9 +318,9 @@ SPLIT_CASES = [("q4k-reg", N.Q4_K, "1"), ("q4k-lds", N.Q4_K, "0"), ("q6k-lds", N
 @pytest.mark.parametrize("kparts", ["3", "5"])
 @pytest.mark.parametrize("acc", [N.ACC_FP32, N.ACC_FP16], ids=["fp32acc", "fp16acc"])
 @pytest.mark.parametrize("name,qtype,reg", SPLIT_CASES, ids=[c[0] for c in SPLIT_CASES])
-def test_prefill_split_k(ctx, monkeypatch, name, qtype, reg, acc, kparts):
-    monkeypatch.setenv("NS_GEMM_KPARTS", kparts)
-    monkeypatch.setenv("NS_GEMM_Q4_REG", reg)
+def test_prefill_split_k(ctx, tune, name, qtype, reg, acc, kparts):
+    tune("gemm_kparts", kparts)
+    tune("gemm_q4_reg", reg)
     cols, rows, batch = 2048, 320, 200
     fast = acc == N.ACC_FP16
     tol = TOL16 if fast else TOL32
@@ -361,12 +369,38 @@ def test_prefill_ffn_full_size(ctx, acc):
     assert np.isfinite(f16_value(hh)).all() and np.isfinite(yy).all()
     tol = TOL32 if acc == N.ACC_FP32 else TOL16
     for r0 in (0, 7040, F - 128):
-        ref = O.gate_up_geglu_prefill(O.ROW_MAJOR, _row_slice(hg, N.Q4_K, D, r0, 128),
-                                      _row_slice(hu, N.Q4_K, D, r0, 128), D, 128, B, x, 0)
+        gs, us = _row_slice(hg, N.Q4_K, D, r0, 128), _row_slice(hu, N.Q4_K, D, r0, 128)
+        ref = O.gate_up_geglu_prefill(O.ROW_MAJOR, gs, us, D, 128, B, x, 0)
         assert rel_err(f16_value(hh[:, r0:r0 + 128]), ref) <= tol
+        if fast:
+            ref16 = O.gate_up_geglu_prefill(O.ROW_MAJOR, gs, us, D, 128, B, x, 1)
+            assert rel_err(f16_value(hh[:, r0:r0 + 128]), ref16) <= TOL16_SAME_PAIR
     for r0 in (0, 1984, D - 128):
-        ref = O.gemm(N.Q6_K, O.ROW_MAJOR, _row_slice(hd, N.Q6_K, F, r0, 128), F, 128, B, hh, 0)
+        ds = _row_slice(hd, N.Q6_K, F, r0, 128)
+        ref = O.gemm(N.Q6_K, O.ROW_MAJOR, ds, F, 128, B, hh, 0)
         assert rel_err(yy[:, r0:r0 + 128], ref) <= tol
+        if fast:
+            assert rel_err(yy[:, r0:r0 + 128], O.gemm(N.Q6_K, O.ROW_MAJOR, ds, F, 128, B, hh, 1)) <= TOL16_SAME
+
+
+@pytest.mark.parametrize("acc", [N.ACC_FP32, N.ACC_FP16], ids=["fp32acc", "fp16acc"])
+def test_prefill_q4k_down_full_size(ctx, acc):
+    """The Q4_K down projection of the Q4_K_M mix (odd layers of config 4) at full size:
+    15360 -> 3840 at batch 1024, 128-row samples against the oracle in the same mode."""
+    D, F, B = 3840, 15360, 1024
+    hd, wd = weights(N.Q4_K, 65, D, F, N.CDNA4)
+    x = N.synth_normal_f16(66, B * F).reshape(B, F)
+    y = torch.empty((B, D), dtype=torch.float32, device="cuda")
+    fast = acc == N.ACC_FP16
+    ctx.ffn_down(wd, N.Q4_K, N.CDNA4, F, D, B, dev_u16(x), y, half_input=True, fast_swa=fast)
+    torch.cuda.synchronize()
+    yy = y.cpu().numpy()
+    assert np.isfinite(yy).all()
+    for r0 in (0, 1984, D - 128):
+        ds = _row_slice(hd, N.Q4_K, F, r0, 128)
+        assert rel_err(yy[:, r0:r0 + 128], O.gemm(N.Q4_K, O.ROW_MAJOR, ds, F, 128, B, x, 0)) <= (TOL16 if fast else TOL32)
+        if fast:
+            assert rel_err(yy[:, r0:r0 + 128], O.gemm(N.Q4_K, O.ROW_MAJOR, ds, F, 128, B, x, 1)) <= TOL16_SAME
 
 
 # ---- device layout conversion and argument errors -------------------------------
@@ -396,3 +430,34 @@ def test_argument_errors(ctx):
     with pytest.raises(N.NsError) as e:  # fp16 input at batch 1 is no regime of matmul (mm:269-275)
         ctx.matmul(w, N.Q4_K, N.CDNA4, 256, 64, 1, x, y, half_input=True)
     assert e.value.code == 4
+
+
+# ---- the reference's own values on the GPU ----------------------------------------------
+
+@pytest.mark.parametrize("layout", LAYOUTS, ids=LNAME.get)
+@pytest.mark.parametrize("name,qtype", [("q4k", N.Q4_K), ("q6k", N.Q6_K)])
+def test_golden_vectors_on_gpu(ctx, name, qtype, layout):
+    """tests/golden/quant_golden.npz holds values and dot_row results written by the reference's
+    own quant.cpp (oracle/_ref): seeded blocks plus extremes (zero and maximal scales, fp16-
+    subnormal d, sc = -32).  The GPU's dequant must equal the values bit for bit and its GEMV
+    must be within the FP32 bar of the reference's dots.  Slab layouts get the 2 golden rows
+    padded to one 64-row slab with zero blocks."""
+    import os
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "quant_golden.npz"))
+    cols, rows = (int(v) for v in z[f"{name}_shape"])
+    raw = z[f"{name}_bytes"]
+    bb = 144 if qtype == N.Q4_K else 210
+    prow = rows if layout == N.ROW_MAJOR else 64
+    host = np.zeros(prow * (cols // 256) * bb, dtype=np.uint8)
+    host[:raw.size] = raw
+    img = host if layout == N.ROW_MAJOR else N.retile(host, qtype, cols, prow, N.ROW_MAJOR, layout)
+    w = torch.from_numpy(np.ascontiguousarray(img)).cuda()
+    out = torch.empty((rows, cols), dtype=torch.float32, device="cuda")
+    ctx.dequant(w, qtype, layout, cols, prow, 0, rows, out_f32=out)
+    y = torch.empty(prow, dtype=torch.float32, device="cuda")
+    ctx.matmul(w, qtype, layout, cols, prow, 1, torch.from_numpy(z[f"{name}_x"]).cuda(), y)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy().reshape(-1).view(np.uint32), z[f"{name}_values"].view(np.uint32))
+    dots = z[f"{name}_dot"].astype(np.float64)
+    got = y.cpu().numpy()[:rows].astype(np.float64)
+    assert np.max(np.abs(got - dots)) <= TOL32 * np.max(np.abs(dots))

@@ -60,16 +60,16 @@ def _weights(qtype, seed, rows, cols, layout):
 
 
 @pytest.mark.parametrize("qtype,layout,cols,rows", CASES, ids=IDS)
-def test_gemv_sweep(ctx, monkeypatch, qtype, layout, cols, rows):
+def test_gemv_sweep(ctx, tune, qtype, layout, cols, rows):
     host, w = _weights(qtype, 300 + rows, rows, cols, layout)
     x = N.synth_normal_f32(301 + cols, cols)
     ref = O.gemv(qtype, O.ROW_MAJOR, host, cols, rows, x)
     xd = torch.from_numpy(x).cuda()
     for pf in (None, "0", "1"):  # the planner's choice, one unit per wave, streaming
         if pf is None:
-            monkeypatch.delenv("NS_GEMV_PF", raising=False)
+            tune("gemv_pf", -1)
         else:
-            monkeypatch.setenv("NS_GEMV_PF", pf)
+            tune("gemv_pf", pf)
         y = torch.full((rows,), float("nan"), dtype=torch.float32, device="cuda")
         ctx.matmul(w, qtype, layout, cols, rows, 1, xd, y)
         torch.cuda.synchronize()

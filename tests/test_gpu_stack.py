@@ -103,7 +103,7 @@ def test_stack_prefill_mode_rule(ctx):
             assert rel_err(f16_value(hh), O.gate_up_geglu_prefill(O.ROW_MAJOR, hg, hu, D, F, B, xh, 0)) <= tol
             assert rel_err(yh, O.gemm(dt, O.ROW_MAJOR, hd, F, D, B, hh, 0)) <= tol
             if fast:
-                assert rel_err(yh, O.gemm(dt, O.ROW_MAJOR, hd, F, D, B, hh, mode)) <= 4e-3
+                assert rel_err(yh, O.gemm(dt, O.ROW_MAJOR, hd, F, D, B, hh, mode)) <= 1e-3
             # FP16 mode leaves fp16 precision (13 low fraction bits clear); FP32 mode does not
             assert (not np.any(yh.view(np.uint32) & 0x1FFF)) == fast, (layer, exact)
             xn = torch.empty((B, D), dtype=torch.int16, device="cuda")
@@ -119,10 +119,12 @@ def test_stack_prefill_mode_rule(ctx):
 @pytest.mark.parametrize("nlayers", [6, 48])
 def test_decode_step_graph_replay_matches_eager(ctx, nlayers):
     """A decode step of the stack (config 4: Q4_K_M down mix, rms fused into every
-    gate/up, the final rms and the lm-head at the end) captured once into a HIP graph
-    and replayed three times, with eager work and synchronisations between replays;
-    every replay's logits must equal the eager step's bit for bit."""
-    D, F, V = 3840, 15360, 65536
+    gate/up, the final rms and the full 262,144-row lm-head at the end) captured once into a
+    HIP graph and replayed three times, with eager work and synchronisations between
+    replays; every replay's logits must equal the eager step's bit for bit.  Between the
+    capture and the replays the same context runs a batch-1024 prefill block in both modes,
+    the largest workspace user: the captured graph's workspace pointers must stay valid."""
+    D, F, V = 3840, 15360, 262144
     layers = []
     for l in range(nlayers):
         s = N.layer_seed(0x6A, l)
@@ -156,9 +158,23 @@ def test_decode_step_graph_replay_matches_eager(ctx, nlayers):
     step()
     torch.cuda.synchronize()
     eager, eager_x = logits.clone(), xd.clone()
+    ws0 = ctx.workspace_bytes()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         step()
+    # prefill on the same context between capture and replay (gate/up + down, Q6_K and Q4_K)
+    B = 1024
+    xp = torch.from_numpy(N.synth_normal_f16(0x6E, B * D).view(np.int16).reshape(B, D)).cuda()
+    hp = torch.empty((B, F), dtype=torch.int16, device="cuda")
+    yp = torch.empty((B, D), dtype=torch.float32, device="cuda")
+    g0, u0, d0, dt0, _ = layers[0]
+    g1, u1, d1, dt1, _ = layers[1]
+    for fast in (False, True):
+        ctx.ffn_block(g0, u0, d0, dt0, N.CDNA4, D, F, B, xp, hp, yp, prefill=True, swa=fast)
+        ctx.ffn_block(g1, u1, d1, dt1, N.CDNA4, D, F, B, xp, hp, yp, prefill=True, swa=fast)
+    torch.cuda.synchronize()
+    assert torch.isfinite(yp).all()
+    assert ctx.workspace_bytes() == ws0, "a model-shape call grew the workspace"
     for r in range(3):
         xd.copy_(x0)
         logits.zero_()
@@ -168,3 +184,62 @@ def test_decode_step_graph_replay_matches_eager(ctx, nlayers):
         assert torch.equal(logits, eager) and torch.equal(xd, eager_x), f"replay {r}"
         step()  # eager work between replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("batch", [2, 4])
+def test_prefill_small_batch_takes_fp32_kernels(ctx, batch):
+    """mm:566-569: a prefill of 2-4 tokens (MTP verification) runs gate_up_geglu and the
+    down projection through matmul's small-batch kernels in FP32 accumulation even on a
+    local (swa) layer: H and Y within the FP32 bar of the FP32 oracle, and Y not rounded to
+    fp16 precision."""
+    D, F = 3840, 15360
+    s = N.layer_seed(0xB2, batch)
+    hg, hu, hd = (N.synth_weights(N.Q4_K, s + 1, F, D), N.synth_weights(N.Q4_K, s + 2, F, D),
+                  N.synth_weights(N.Q6_K, s + 3, D, F))
+    wg, wu, wd = cdna4(hg, N.Q4_K, F, D), cdna4(hu, N.Q4_K, F, D), cdna4(hd, N.Q6_K, D, F)
+    xh = N.synth_normal_f16(s + 4, batch * D).reshape(batch, D)
+    x = torch.from_numpy(xh.view(np.int16)).cuda()
+    hp = torch.empty((batch, F), dtype=torch.int16, device="cuda")
+    yp = torch.empty((batch, D), dtype=torch.float32, device="cuda")
+    ctx.ffn_block(wg, wu, wd, N.Q6_K, N.CDNA4, D, F, batch, x, hp, yp, prefill=True, swa=True)
+    torch.cuda.synchronize()
+    hh = hp.cpu().numpy().view(np.uint16)
+    yh = yp.cpu().numpy()
+    assert rel_err(f16_value(hh), O.gate_up_geglu_prefill(O.ROW_MAJOR, hg, hu, D, F, batch, xh, 0)) <= TOL32
+    assert rel_err(yh, O.gemm(N.Q6_K, O.ROW_MAJOR, hd, F, D, batch, hh, 0)) <= TOL32
+    assert np.any(yh.view(np.uint32) & 0x1FFF)
+
+
+def test_prefill_48_layers_full_size_finite(ctx):
+    """Config 4's prefill at full size: 48 distinct seeded layers at batch 1024 with the
+    Q4_K_M down mix and the mode rule (layers 5, 11, ... FP32, the rest FP16), chained through
+    rms_half with seeded sign weights.  Every layer's Y must be finite and non-zero, and the
+    first two layers' outputs are checked against the oracle on 64-row samples."""
+    D, F, B = 3840, 15360, 1024
+    x = torch.from_numpy(N.synth_normal_f16(0x48, B * D).view(np.int16).reshape(B, D)).cuda()
+    hp = torch.empty((B, F), dtype=torch.int16, device="cuda")
+    yp = torch.empty((B, D), dtype=torch.float32, device="cuda")
+    for layer in range(48):
+        s = N.layer_seed(0xC4, layer)
+        dt = N.Q6_K if layer % 2 == 0 else N.Q4_K
+        glob = layer % 6 == 5
+        hg, hu, hd = (N.synth_weights(N.Q4_K, s + 1, F, D), N.synth_weights(N.Q4_K, s + 2, F, D),
+                      N.synth_weights(dt, s + 3, D, F))
+        wg, wu, wd = cdna4(hg, N.Q4_K, F, D), cdna4(hu, N.Q4_K, F, D), cdna4(hd, dt, D, F)
+        ctx.ffn_block(wg, wu, wd, dt, N.CDNA4, D, F, B, x, hp, yp, prefill=True, swa=not glob)
+        torch.cuda.synchronize()
+        assert torch.isfinite(yp).all() and torch.any(yp != 0), layer
+        if layer < 2:
+            xh = x.cpu().numpy().view(np.uint16)
+            hh = hp.cpu().numpy().view(np.uint16)
+            mode = 0 if glob else 1
+            gs = hg.reshape(F, -1)[:64].reshape(-1)
+            us = hu.reshape(F, -1)[:64].reshape(-1)
+            assert rel_err(f16_value(hh[:, :64]), O.gate_up_geglu_prefill(O.ROW_MAJOR, gs, us, D, 64, B, xh, mode)) <= 5e-3
+            ds = hd.reshape(D, -1)[:64].reshape(-1)
+            assert rel_err(yp.cpu().numpy()[:, :64], O.gemm(dt, O.ROW_MAJOR, ds, F, 64, B, hh, mode)) <= 1e-3
+        nw = signs(N.layer_seed(0xC4, layer + 1) + 5, D)
+        xn = torch.empty((B, D), dtype=torch.int16, device="cuda")
+        ctx.rmsnorm(yp, torch.from_numpy(nw).cuda(), B, D, EPS, xn, half_out=True)
+        x = xn
+    torch.cuda.synchronize()

@@ -271,3 +271,118 @@ def test_rmsnorm_add_and_then():
     y, nxt = O.rmsnorm(x, w, residual=res, scale=0.75, next_w=nw, eps=1e-6)
     np.testing.assert_array_equal(y, O.rmsnorm(x, w, residual=res, scale=0.75, eps=1e-6))
     np.testing.assert_array_equal(nxt, O.rmsnorm(y, nw, eps=1e-6))
+
+
+# ---- the FP16 mode: fp16 tiles with a row scale, one rounding at the end ----------------
+
+def _q4_rows(specs):
+    """Q4_K rows from (d, dmin, sc[8], m[8], q[256]) per block: spec[r] = list of blocks."""
+    return np.concatenate([np.concatenate([q4k_block(*blk) for blk in row]) for row in specs])
+
+
+def test_f16_tile_equals_reference_half_form_on_power_of_two_factors():
+    """With d and dmin powers of two, A = d*sc*2^24*c and B = -dmin*m*c are exact in fp16, so
+    the tile is one rounding of c*(d*sc*q - dmin*m) and F/c equals the reference's
+    half(d*sc*q - dmin*m) (metal:231) bit for bit.  Q6_K likewise with half(d*sc*(v-32))
+    (metal:417-418).  Random quants and scales, factors 2^-12..2^-6."""
+    rng = _rng(21)
+    cols, rows = 512, 8
+    specs = []
+    for r in range(rows):
+        blocks = []
+        for b in range(cols // 256):
+            blocks.append((2.0 ** -int(rng.integers(6, 13)), 2.0 ** -int(rng.integers(6, 13)),
+                           rng.integers(0, 64, 8), rng.integers(0, 64, 8), rng.integers(0, 16, 256)))
+        specs.append(blocks)
+    w = _q4_rows(specs)
+    tile, inv = O.f16_tile_rows(O.Q4_K, O.ROW_MAJOR, w, cols, rows)
+    exact = O.dequant_rows(O.Q4_K, O.ROW_MAJOR, w, cols, rows)
+    np.testing.assert_array_equal(tile * inv[:, None], exact.astype(np.float16).astype(np.float32))
+    w6 = _random_blocks(O.Q6_K, rows * cols // 256, seed=22).reshape(-1, 210)
+    w6[:, 208:210] = np.array([2.0 ** -int(e) for e in rng.integers(6, 13, len(w6))],
+                              dtype=np.float16).view(np.uint8).reshape(-1, 2)
+    w6 = w6.reshape(-1)
+    tile, inv = O.f16_tile_rows(O.Q6_K, O.ROW_MAJOR, w6, cols, rows)
+    exact = O.dequant_rows(O.Q6_K, O.ROW_MAJOR, w6, cols, rows)
+    np.testing.assert_array_equal(tile * inv[:, None], exact.astype(np.float16).astype(np.float32))
+
+
+def test_f16_tile_known_roundings():
+    """Hand-computed values.  d = 1 + 2^-10, dmin = 0.5: M = d, ceil(log2 M) = 1, c = 2^-16,
+    c*2^24 = 256.  Group 0 (sc = 63, m = 63): A = RNE16(63.0615234375 * 256 = 16143.75) = 16144
+    (ulp 8); B = -0.5*63*2^-16 = -2016 * 2^-22 (exact).  q = 15: q*2^-24*A + B =
+    0.013953208923339844 = 1828.875 ulps of 2^-17 -> RNE16 = 1829 * 2^-17.  q = 0 gives B
+    itself; a block with d = dmin = 0 gives zeros."""
+    sc = np.array([63, 1, 2, 3, 4, 5, 6, 7])
+    m = np.array([63, 0, 0, 0, 0, 0, 0, 0])
+    q = np.zeros(256, dtype=np.int64)
+    q[0], q[1] = 15, 0
+    w = _q4_rows([[(1.0 + 2.0 ** -10, 0.5, sc, m, q), (0.0, 0.0, np.zeros(8, int), np.zeros(8, int),
+                                                        np.zeros(256, int))]])
+    tile, inv = O.f16_tile_rows(O.Q4_K, O.ROW_MAJOR, w, 512, 1)
+    assert inv[0] == 2.0 ** 16
+    A = 16144.0
+    B = -2016.0 * 2.0 ** -22
+    v = 15 * 2.0 ** -24 * A + B
+    assert v / 2.0 ** -17 == 1828.875
+    assert tile[0, 0] == np.float32(1829 * 2.0 ** -17)
+    assert tile[0, 1] == np.float32(B)
+    assert not np.any(tile[0, 256:])
+    # the row scale at and just past a power of two: M = 2 -> c*2^24 = 2^8; M = 2 + 2^-9 -> 2^7
+    for dv, expect in ((2.0, 2.0 ** (15 + 1)), (2.0 + 2.0 ** -9, 2.0 ** (15 + 2)), (2.0 ** -24, 2.0 ** -9)):
+        w1 = _q4_rows([[(dv, 0.0, sc, np.zeros(8, int), q)]])
+        _, inv1 = O.f16_tile_rows(O.Q4_K, O.ROW_MAJOR, w1, 256, 1)
+        assert inv1[0] == np.float32(expect), (dv, inv1[0])
+    # a zero row: c = 1 and zero tiles
+    wz = _q4_rows([[(0.0, 0.0, sc, m, q)]])
+    tz, iz = O.f16_tile_rows(O.Q4_K, O.ROW_MAJOR, wz, 256, 1)
+    assert iz[0] == 1.0 and not np.any(tz)
+
+
+def test_f16_tile_error_bound():
+    """On BASELINE-distributed blocks, F/c differs from the exact weight w by at most the three
+    roundings of A, B and F: |F/c - w| <= 2^-11 * (|d*sc*q| + |dmin*m| + |w|) * (1 + 2^-10)
+    plus the subnormal step 2^-24/c, bounded here through |d*sc*q| <= |w| + 63|dmin| (Q6_K:
+    |d*sc*v| + 32|d*sc| <= |w| + 64*32|d|).  A wrong row scale, a dropped B or a q off by one
+    breaks this by the size of a weight."""
+    nsffn = pytest.importorskip("nsffn")
+    cols, rows = 3840, 64
+    for qt in (O.Q4_K, O.Q6_K):
+        w = nsffn.synth_weights(qt, 23 + qt, rows, cols)
+        tile, inv = O.f16_tile_rows(qt, O.ROW_MAJOR, w, cols, rows)
+        exact = O.dequant_rows(qt, O.ROW_MAJOR, w, cols, rows).astype(np.float64)
+        got = tile.astype(np.float64) * inv[:, None]
+        blocks = w.reshape(rows, cols // 256, 144 if qt == O.Q4_K else 210)
+        if qt == O.Q4_K:
+            side = 63 * np.abs(blocks[:, :, 2:4].copy().view(np.float16).astype(np.float64))  # 63|dmin|
+            terms = 2 * np.abs(exact) + 2 * np.repeat(side[:, :, 0], 256, axis=1)
+        else:
+            dd = np.abs(blocks[:, :, 208:210].copy().view(np.float16).astype(np.float64))
+            terms = 2 * np.abs(exact) + 64 * 32 * np.repeat(dd[:, :, 0], 256, axis=1)
+        bound = 2.0 ** -11 * (1 + 2.0 ** -10) * terms + 2.0 ** -24 * inv[:, None].astype(np.float64)
+        assert np.all(np.abs(got - exact) <= bound), qt
+
+
+def test_fp16_mode_rounds_once_at_the_end():
+    """Integer sums (every product and partial sum exact): one row whose block 0 sums to 2049
+    and block 1 to 1.  x = 1 on both blocks: FP32 mode 2050; FP16 mode RNE11(2050) = 2050 (one
+    rounding at the end; rounding per super-block would give RNE11(RNE11(2049) + 1) = 2048).
+    x = 1 on block 0 only: FP32 2049, FP16 RNE11(2049) = 2048 (the tie goes to even)."""
+    sc1, m0 = np.ones(8, int), np.zeros(8, int)
+    q0 = np.zeros(256, dtype=np.int64)
+    q0[:136] = 15
+    q0[136] = 9
+    q1 = np.zeros(256, dtype=np.int64)
+    q1[0] = 1
+    row0 = [(1.0, 0.0, sc1, m0, q0), (1.0, 0.0, sc1, m0, q1)]
+    zero = [(0.0, 0.0, m0, m0, np.zeros(256, int))] * 2
+    w = _q4_rows([row0, zero])
+    x = np.zeros((2, 512), dtype=np.float16)
+    x[0, :] = 1
+    x[1, :256] = 1
+    xb = f16_bits(x)
+    y32 = O.gemm(O.Q4_K, O.ROW_MAJOR, w, 512, 2, 2, xb, 0)
+    y16 = O.gemm(O.Q4_K, O.ROW_MAJOR, w, 512, 2, 2, xb, 1)
+    assert y32[0, 0] == 2050 and y32[1, 0] == 2049
+    assert y16[0, 0] == 2050 and y16[1, 0] == 2048
+    assert not np.any(y32[:, 1]) and not np.any(y16[:, 1])
