@@ -100,6 +100,18 @@ int ns_ctx_set_tuning(ns_ctx *ctx, const char *key, int value);
 int ns_matmul(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, uint32_t rows,
               uint32_t batch, const void *in, int half_input, float *out, void *stream);
 
+/* No counterpart in the reference: ns_matmul for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops and harnesses that forbid hipMalloc).  The same
+ * regimes and kernels as ns_matmul with the default tuning, without a context: the split
+ * reductions use a static device scratch array of 16 MiB of parts and 65,536 counters that
+ * each GPU holds until the process ends; a shape that needs more fails with
+ * NS_ERR_UNSUPPORTED (every decode GEMV and small-batch shape of the reference model fits;
+ * large prefill GEMMs do not).  fp32 input above batch 4 is refused.  Calls that overlap on
+ * one GPU share the array and race: order them (one stream).  Allocates nothing, never
+ * synchronises, and may be captured into a graph. */
+int ns_matmul_noalloc(const void *w, int type, int layout, uint32_t cols, uint32_t rows, uint32_t batch,
+                      const void *in, int half_input, float *out, void *stream);
+
 /* gate_up_geglu_decode (mm:290): h[r] = gelu_tanh(Wg[r].x) * (Wu[r].x), fp32, Q4_K gate/up. */
 int ns_gate_up_geglu_decode(ns_ctx *ctx, const void *wg, const void *wu, int layout,
                             uint32_t cols, uint32_t rows, const float *x, float *h,

@@ -66,6 +66,7 @@ def lib():
             "ns_ctx_workspace_bytes": [vp, ctypes.POINTER(u64)],
             "ns_ctx_set_tuning": [vp, ctypes.c_char_p, i32],
             "ns_matmul": [vp, vp, i32, i32, u32, u32, u32, vp, i32, vp, vp],
+            "ns_matmul_noalloc": [vp, i32, i32, u32, u32, u32, vp, i32, vp, vp],
             "ns_gate_up_geglu_decode": [vp, vp, vp, i32, u32, u32, vp, vp, vp],
             "ns_gate_up_geglu_rm32": [vp, vp, vp, i32, u32, u32, u32, vp, vp, i32, vp],
             "ns_gate_up_geglu": [vp, vp, vp, i32, u32, u32, u32, vp, vp, vp],
@@ -431,6 +432,12 @@ class Context:
     def dequant(self, w, qtype, layout, cols, rows, row0, nrows, out_f32=None, out_f16=None, stream=None):
         check(lib().ns_dequant(self.handle, _ptr(w), qtype, layout, cols, rows, row0, nrows,
                                _ptr(out_f32), _ptr(out_f16), _stream(stream)))
+
+
+def matmul_noalloc(w, qtype, layout, cols, rows, batch, inp, out, half_input=False, stream=None):
+    """ns_matmul_noalloc: ns_matmul on the library's static device scratch (no context)."""
+    check(lib().ns_matmul_noalloc(_ptr(w), qtype, layout, cols, rows, batch, _ptr(inp), int(half_input), _ptr(out),
+                                  _stream(stream)))
 
 
 def retile_device(src, dst, qtype, cols, rows, from_layout, to_layout, stream=None):
