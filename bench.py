@@ -17,10 +17,15 @@ Also reported under "extra":
             pair and Q6_K down (fp16 x), weights streamed once for all tokens;
             beside it, the lm-head as one GEMV per token.
 
+The CPU leg (skipped by --no-cpu) times the oracle on the host cores: config 1 as the
+line's cpu_baseline, and beside configs 0, 2, 3 (both modes) and 4's decode step in
+"extra" (cpu_* keys), each on a bounded sample named in cpu_samples.
+
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--only all|headline|lmhead|prefill|stack|smallbatch]
+                       [--only all|headline|lmhead|pmc|prefill|stack|smallbatch]
   --only lmhead runs just the lm-head GEMV (K launches) and a 256 MiB device copy
   of known size: the driver for the rocprofv3 --pmc traffic runs.
+  --only pmc does the same for the prefill GEMMs and the small decode GEMVs.
 """
 import argparse
 import json
@@ -42,6 +47,7 @@ D, F, V, B = 3840, 15360, 262144, 1024
 NLAYERS, DECODE_STEPS = 48, 64
 EPS = 1e-6  # the RMSNorm epsilon of the stack (Gemma's)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic_lm_head_gemv.md")
+PMC_GEMM_FILE = os.path.join(ROOT, "profiles", "pmc_prefill_gemm.md")
 
 
 def qbytes(qtype, rows, cols):
@@ -127,6 +133,17 @@ def measured_traffic():
         return int(m.group(1)) if m else None
     except OSError:
         return None
+
+
+def pmc_figures():
+    """MFMA utilisation, clock and fetch ratios of the prefill GEMMs and decode GEMVs from the
+    committed rocprofv3 --pmc summary (lines `name: value`), or {}."""
+    try:
+        text = open(PMC_GEMM_FILE).read()
+    except OSError:
+        return {}
+    return {k: float(v) for k, v in re.findall(
+        r"^\s+((?:mfma_util|clock_ghz|mfma_instr_check|fetch_over_algorithmic)_\w+): ([0-9.]+)$", text, re.M)}
 
 
 class Bench:
@@ -251,6 +268,64 @@ class Bench:
         log(f"cpu baseline {cpu['value']} GB/s in {dt:.2f}s; parity {self.extra['parity_rel_err_down']:.2e} "
             f"{self.extra['parity_rel_err_lm_head']:.2e}")
         return cpu
+
+    def cpu_extra(self):
+        """The oracle beside configs 0, 2, 3 and 4, each on a bounded sample (a few seconds):
+        the same seeded shapes and distributions as the GPU legs, the same oracle as the
+        headline's cpu_baseline, threaded over rows on the host cores."""
+        N = self.N
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import ns_oracle as O
+
+        nt = N.default_threads()
+
+        def rate(fn, budget_s):
+            reps, t = 0, time.perf_counter()
+            while True:
+                fn()
+                reps += 1
+                dt = time.perf_counter() - t
+                if dt >= budget_s:
+                    return dt / reps  # s per call
+        g = N.synth_weights(Q4, 0x60, F, D)
+        u = N.synth_weights(Q4, 0x61, F, D)
+        d6 = N.synth_weights(Q6, 0x62, D, F)
+        d4 = N.synth_weights(Q4, 0x63, D, F)
+        x, hx = N.synth_normal_f32(0x64, D), N.synth_normal_f32(0x65, F)
+        samples = {}
+        # config 0: the Q4_K GEMV
+        t0 = rate(lambda: O.gemv(Q4, O.ROW_MAJOR, g, D, F, x, nthreads=nt), 2.0)
+        self.extra.update(cpu_cfg0_q4k_gemv_us=round(t0 * 1e6, 1), cpu_cfg0_q4k_gemv_GBps=round(BYTES_Q4_GATE / t0 / 1e9, 3))
+        samples["cfg0"] = "whole GEMVs"
+        # config 2: one decode FFN block (gate/up + GeGLU, Q6_K down)
+        t_gu = rate(lambda: O.gate_up_geglu(O.ROW_MAJOR, g, u, D, F, x, nthreads=nt), 2.0)
+        t_d6 = rate(lambda: O.gemv(Q6, O.ROW_MAJOR, d6, F, D, hx, nthreads=nt), 2.0)
+        t_d4 = rate(lambda: O.gemv(Q4, O.ROW_MAJOR, d4, F, D, hx, nthreads=nt), 1.0)
+        self.extra.update(cpu_cfg2_ffn_block_decode_us=round((t_gu + t_d6) * 1e6, 1),
+                          cpu_cfg2_ffn_block_decode_GBps=round(BYTES_FFN_LAYER / (t_gu + t_d6) / 1e9, 3))
+        samples["cfg2"] = "one block (gate/up pair then Q6_K down), repeated; per block"
+        # config 3: the prefill block on a sample of tokens, both modes
+        T = 32
+        xs = N.synth_normal_f16(0x66, T * D)
+        hs = N.synth_normal_f16(0x67, T * F)
+        for acc, name in ((0, "fp32acc"), (1, "fp16acc")):
+            t = rate(lambda: (O.gate_up_geglu_prefill(O.ROW_MAJOR, g, u, D, F, T, xs, acc, nthreads=nt),
+                              O.gemm(Q6, O.ROW_MAJOR, d6, F, D, T, hs, acc, nthreads=nt)), 2.0)
+            self.extra[f"cpu_cfg3_prefill_{name}_tokens_per_s"] = round(T / t, 1)
+        samples["cfg3"] = f"{T} of the 1024 tokens through a whole block (gate/up pair then Q6_K down), per mode"
+        # config 4: the decode step = 24 layers with a Q6_K down + 24 with a Q4_K down + the lm-head
+        lm = self.lm_host if hasattr(self, "lm_host") else N.synth_weights(Q6, 0x1B, V, D)
+        t_lm = rate(lambda: O.gemv(Q6, O.ROW_MAJOR, lm, D, V, x, nthreads=nt), 1.0)
+        step = (NLAYERS // 2) * (2 * t_gu + t_d6 + t_d4) + t_lm
+        self.extra.update(cpu_cfg4_decode_ms_per_step=round(step * 1e3, 2))
+        samples["cfg4"] = ("decode step composed of the timed gate/up pair, Q6_K and Q4_K downs and lm-head GEMVs "
+                           "(24 layers of each down type + the lm-head); the RMSNorms are not counted")
+        self.extra["cpu_cores"] = nt
+        self.extra["cpu_model"] = cpu_model()
+        self.extra["cpu_samples"] = samples
+        log(f"cpu extra: cfg0 {t0 * 1e6:.0f} us, cfg2 {(t_gu + t_d6) * 1e6:.0f} us/block, cfg3 "
+            f"{self.extra['cpu_cfg3_prefill_fp32acc_tokens_per_s']}/{self.extra['cpu_cfg3_prefill_fp16acc_tokens_per_s']}"
+            f" tok/s, cfg4 {step * 1e3:.1f} ms/step")
 
     # -- config 0 and 3 ------------------------------------------------------------
     def config0(self):
@@ -418,6 +493,46 @@ class Bench:
             f"{step_bytes / (g_ms * 1e-3) / 1e9:.1f} GB/s; graph replay == eager: {replay_equal}")
 
     # -- PMC driver -----------------------------------------------------------------------
+    def pmc_driver(self):
+        """The launch sequence the rocprofv3 --pmc passes read: every prefill GEMM instance at
+        batch 1024 (gate/up pair, Q6_K and Q4_K down; FP32 then FP16 mode), the decode GEMVs
+        (config 0's Q4_K, config 1's Q6_K down, the gate/up pair), --steps launches each, then
+        three copies of a 256 MiB buffer, the copy of known size that scales FETCH_SIZE and
+        WRITE_SIZE.  Weights rotate over two copies so a launch cannot find the previous one's
+        weights in the Infinity Cache."""
+        N, torch, ctx, n = self.N, self.torch, self.ctx, self.args.steps
+        g = [self.weights(Q4, 0x90 + i, F, D) for i in range(2)]
+        u = [self.weights(Q4, 0x92 + i, F, D) for i in range(2)]
+        d6 = [self.weights(Q6, 0x94 + i, D, F) for i in range(2)]
+        d4 = [self.weights(Q4, 0x98 + i, D, F) for i in range(2)]
+        xp = self.f16(0x96, B * D)
+        hp = torch.empty((B, F), dtype=torch.int16, device="cuda")
+        hpin = self.f16(0x97, B * F)
+        yp = torch.empty((B, D), dtype=torch.float32, device="cuda")
+        xd, hd = self.f32(0x61, D), self.f32(0x72, F)
+        yd, hdo = torch.empty(F, dtype=torch.float32, device="cuda"), torch.empty(F, dtype=torch.float32, device="cuda")
+        yd2 = torch.empty(D, dtype=torch.float32, device="cuda")
+        a = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        for fast in (False, True):
+            for i in range(n):
+                ctx.gate_up_geglu_rm32(g[i % 2], u[i % 2], N.CDNA4, D, F, B, xp, hp, fast)
+            for i in range(n):
+                ctx.ffn_down(d6[i % 2], Q6, N.CDNA4, F, D, B, hpin, yp, True, fast)
+            for i in range(n):
+                ctx.ffn_down(d4[i % 2], Q4, N.CDNA4, F, D, B, hpin, yp, True, fast)
+        for i in range(n):
+            ctx.matmul(g[i % 2], Q4, N.CDNA4, D, F, 1, xd, yd)
+        for i in range(n):
+            ctx.matmul(d6[i % 2], Q6, N.CDNA4, F, D, 1, hd, yd2)
+        for i in range(n):
+            ctx.gate_up_geglu_decode(g[i % 2], u[i % 2], N.CDNA4, D, F, xd, hdo)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log(f"pmc driver: {n} launches of each prefill GEMM (both modes) and decode GEMV, 3 x 256 MiB copies")
+
     def lmhead_only(self):
         N, torch, ctx = self.N, self.torch, self.ctx
         lm = self.weights(Q6, 0x1B, V, D)
@@ -444,7 +559,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--quick", action="store_true", help="same as --only headline")
-    ap.add_argument("--only", default="all", choices=["all", "headline", "lmhead", "prefill", "stack", "smallbatch"])
+    ap.add_argument("--only", default="all",
+                    choices=["all", "headline", "lmhead", "pmc", "prefill", "stack", "smallbatch"])
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {args.gpus}); how the path would shard is described "
@@ -454,6 +570,9 @@ def main():
     bench = Bench(args)
     if only == "lmhead":
         bench.lmhead_only()
+        return
+    if only == "pmc":
+        bench.pmc_driver()
         return
     if only == "prefill":
         bench.config3()
@@ -474,6 +593,8 @@ def main():
         bench.smallbatch()
         bench.stack()
     cpu = None if args.no_cpu else bench.cpu_baseline()
+    if cpu is not None and only == "all":
+        bench.cpu_extra()
     out = {
         "metric": METRIC,
         "value": round(bench.value, 1),
@@ -494,7 +615,7 @@ def main():
                      "frac": round(bench.lm_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "gemv_kernel<Q6_K, CDNA4> (lm-head, 826,817,536 algorithmic bytes per launch)"},
         "cpu_baseline": cpu,
-        "extra": bench.extra,
+        "extra": dict(bench.extra, pmc=pmc_figures(), pmc_source="profiles/pmc_prefill_gemm.md"),
     }
     print(json.dumps(out), flush=True)
     bench.ctx.close()
