@@ -84,7 +84,10 @@ int ns_ctx_workspace_bytes(const ns_ctx *ctx, uint64_t *bytes);
  * force the one-unit / prefetching decode GEMV), "gemv_waves" (> 0: the
  * prefetching GEMV's flattened grid), "gemv_whole" / "gemv_qslab" (0 disables
  * that decode grid), "gemm_kparts" (> 0: split-K parts of the prefill GEMM),
- * "gemm_q4_reg" (0: the LDS-tile Q4_K GEMM).  Results stay within the same
+ * "gemm_q4_reg" (0: the LDS-tile Q4_K GEMM), "mt_mfma" (0: batch 1-4 of the
+ * CDNA4 layout on the VALU kernel instead of the matrix cores), "mt_parts" /
+ * "mt_slabs" / "mt_spw" (> 0: that MFMA kernel's column parts per workgroup,
+ * slabs per workgroup, super-blocks per wave).  Results stay within the same
  * tolerances; engines leave the defaults. */
 int ns_ctx_set_tuning(ns_ctx *ctx, const char *key, int value);
 

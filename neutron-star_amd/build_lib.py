@@ -16,7 +16,7 @@ LIB = os.path.join(PKG, "libnsffn.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["ns_host.cpp", "ns_capi.cpp", "ns_nsmffn.cpp", "ns_gguf.cpp", "ns_dequant.hip", "ns_gemv.hip", "ns_gemm.hip", "ns_gemm_reg.hip", "ns_gemm_f16.hip", "ns_norm.hip", "ns_static.hip"]
+SOURCES = ["ns_host.cpp", "ns_capi.cpp", "ns_nsmffn.cpp", "ns_gguf.cpp", "ns_dequant.hip", "ns_gemv.hip", "ns_gemm.hip", "ns_gemm_reg.hip", "ns_gemm_f16.hip", "ns_gemv_mfma.hip", "ns_norm.hip", "ns_static.hip"]
 
 # Packed-fp32 VALU forms are disabled for all device code.
 FLAGS = [

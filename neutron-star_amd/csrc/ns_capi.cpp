@@ -201,6 +201,10 @@ extern "C" int ns_ctx_set_tuning(ns_ctx *ctx, const char *key, int value) {
     else if (k == "gemv_qslab") t.gemv_qslab = value;
     else if (k == "gemm_kparts") t.gemm_kparts = value;
     else if (k == "gemm_q4_reg") t.gemm_q4_reg = value;
+    else if (k == "mt_mfma") t.mt_mfma = value;
+    else if (k == "mt_parts") t.mt_parts = value;
+    else if (k == "mt_slabs") t.mt_slabs = value;
+    else if (k == "mt_spw") t.mt_spw = value;
     else return fail(NS_ERR_ARG, "ns_ctx_set_tuning: unknown key " + k);
     return NS_OK;
 }

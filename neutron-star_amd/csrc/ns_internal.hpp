@@ -22,6 +22,10 @@ struct Tuning {
     int gemv_qslab = 1;   // 0: no k-workgroups-per-slab grid
     int gemm_kparts = 0;  // > 0: the prefill GEMM's split-K parts
     int gemm_q4_reg = 1;  // 0: the LDS-tile Q4_K GEMM instead of the register-fragment one
+    int mt_mfma = 1;      // 0: batch 1-4 of the CDNA4 layout on the VALU kernel instead of MFMA
+    int mt_parts = 0;     // > 0: the batch 1-4 MFMA kernel's column parts per workgroup
+    int mt_slabs = 0;     // > 0: its slabs per workgroup (when the columns are not split)
+    int mt_spw = 0;       // > 0: its super-blocks per wave (more workgroups per slab)
 };
 
 // Workspace owned by ns_ctx: fp32 partial sums and per-slab arrival counters
@@ -61,6 +65,14 @@ void gemv_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, boo
 hipError_t launch_gemv_mt(int type, int layout, const uint8_t *w, const uint8_t *up, const void *x, bool xh,
                           uint32_t batch, void *out, uint32_t cols, uint32_t rows, const Workspace &ws,
                           hipStream_t stream);
+// Batch 1-4 on the matrix cores (ns_gemv_mfma.hip), CDNA4 layout; launch_gemv_mt routes there
+// when gemv_mfma_eligible.
+bool gemv_mfma_eligible(int layout, bool pair, bool xh, const Tuning &t);
+void gemv_mfma_workspace_need(uint32_t cols, uint32_t rows, bool pair, const Tuning &t, size_t *partial_floats,
+                              size_t *counters);
+hipError_t launch_gemv_mfma(int type, const uint8_t *w, const uint8_t *up, const void *x, bool xh, uint32_t batch,
+                            void *out, uint32_t cols, uint32_t rows, const Workspace &ws, hipStream_t stream);
+
 void gemv_mt_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, bool pair, uint32_t batch, bool xh,
                             const Tuning &t, size_t *partial_floats, size_t *counters);
 

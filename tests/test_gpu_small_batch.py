@@ -9,7 +9,7 @@ import pytest
 
 import ns_oracle as O
 import nsffn as N
-from helpers import f16_value, rel_err
+from helpers import f16_value, q6k_block, rel_err
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -113,3 +113,104 @@ def test_lm_head_batch4(ctx):
         sl = _row_slice(host, N.Q6_K, D, r0, 128)
         for t in range(B):
             assert rel_err(got[t, r0:r0 + 128], O.gemv(N.Q6_K, O.ROW_MAJOR, sl, D, 128, xf[t])) <= TOL32, (r0, t)
+
+
+# ---- the MFMA form (ns_gemv_mfma.hip, CDNA4 layout; mt_mfma = 0 selects the VALU kernel) ----
+
+def _both_kernels(ctx, tune, fn):
+    """fn() run on the MFMA kernel and on the VALU kernel (host copies)."""
+    a = fn()
+    tune("mt_mfma", 0)
+    b = fn()
+    tune("mt_mfma", 1)
+    return a, b
+
+
+@pytest.mark.parametrize("half", [False, True], ids=["f32in", "f16in"])
+@pytest.mark.parametrize("qtype", [N.Q4_K, N.Q6_K], ids=["q4k", "q6k"])
+def test_mfma_matches_valu_kernel_full_size(ctx, tune, qtype, half):
+    """Full-size shapes of the model (15360 x 3840 and the 60-block down, which splits its
+    columns over four workgroups), batch 3: the MFMA form against the oracle and within
+    1e-5 of the VALU kernel, whose per-token FMA order is the single-token GEMV's."""
+    for rows, cols in ((15360, 3840), (3840, 15360)):
+        host, w = weights(qtype, 0x5A + rows % 7, rows, cols, N.CDNA4)
+        xd, xf = tokens(0x5B, 3, cols, half)
+
+        def run():
+            y = torch.full((3, rows), float("nan"), dtype=torch.float32, device="cuda")
+            ctx.matmul(w, qtype, N.CDNA4, cols, rows, 3, xd, y, half_input=half)
+            torch.cuda.synchronize()
+            return y.cpu().numpy()
+        got, valu = _both_kernels(ctx, tune, run)
+        assert rel_err(got, valu) <= 1e-5, (rows, cols)
+        for t in range(3):
+            sl = _row_slice(host, qtype, cols, rows - 128, 128)
+            assert rel_err(got[t, rows - 128:], O.gemv(qtype, O.ROW_MAJOR, sl, cols, 128, xf[t])) <= TOL32, (rows, t)
+
+
+@pytest.mark.parametrize("parts", [1, 2, 3, 5])
+def test_mfma_column_parts(ctx, tune, parts):
+    """Every column split of one workgroup (and four workgroups per slab for the 60-block
+    down) gives the oracle's values: the gate/up pair and the Q6_K down at batch 4."""
+    tune("mt_parts", parts)
+    cols, rows = 3840, 256
+    hg, wg = weights(N.Q4_K, 0x61, rows, cols, N.CDNA4)
+    hu, wu = weights(N.Q4_K, 0x62, rows, cols, N.CDNA4)
+    xd, xf = tokens(0x63, 4, cols, True)
+    h = torch.zeros((4, rows), dtype=torch.int16, device="cuda")
+    ctx.gate_up_geglu(wg, wu, N.CDNA4, cols, rows, 4, xd, h)
+    hd, w6 = weights(N.Q6_K, 0x64, 256, 15360, N.CDNA4)
+    xd6, xf6 = tokens(0x65, 4, 15360, True)
+    y = torch.empty((4, 256), dtype=torch.float32, device="cuda")
+    ctx.ffn_down(w6, N.Q6_K, N.CDNA4, 15360, 256, 4, xd6, y, half_input=True, fast_swa=False)
+    torch.cuda.synchronize()
+    got = f16_value(h.cpu().numpy().view(np.uint16))
+    yg = y.cpu().numpy()
+    for t in range(4):
+        assert rel_err(got[t], O.gate_up_geglu(O.ROW_MAJOR, hg, hu, cols, rows, xf[t])) <= TOL32, t
+        assert rel_err(yg[t], O.gemv(N.Q6_K, O.ROW_MAJOR, hd, 15360, 256, xf6[t])) <= TOL32, t
+
+
+def test_mfma_q6k_full_range_scales(ctx):
+    """Real Q6_K tensors carry int8 scales up to +-127 (the synthetic ones stay in -32..31):
+    every scale and every 6-bit value at its extremes, against the oracle."""
+    cols, rows = 1024, 128
+    rng = np.random.default_rng(0x66)
+    nb = rows * cols // 256
+    blocks = []
+    for i in range(nb):
+        sc = rng.integers(-128, 128, 16)
+        sc[i % 16] = -128 if i % 2 else 127
+        v = rng.integers(0, 64, 256)
+        v[:8] = 63
+        v[8:16] = 0
+        blocks.append(q6k_block(np.float16(rng.uniform(1e-4, 2e-3)), sc, v))
+    host = np.concatenate(blocks)
+    w = torch.from_numpy(N.retile(host, N.Q6_K, cols, rows, N.ROW_MAJOR, N.CDNA4)).cuda()
+    for half in (False, True):
+        xd, xf = tokens(0x67, 4, cols, half)
+        y = torch.empty((4, rows), dtype=torch.float32, device="cuda")
+        ctx.matmul(w, N.Q6_K, N.CDNA4, cols, rows, 4, xd, y, half_input=half)
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()
+        for t in range(4):
+            assert rel_err(got[t], O.gemv(N.Q6_K, O.ROW_MAJOR, host, cols, rows, xf[t])) <= TOL32, (half, t)
+
+
+@pytest.mark.parametrize("qtype", [N.Q4_K, N.Q6_K], ids=["q4k", "q6k"])
+def test_mfma_fp32_tokens_beyond_fp16_range(ctx, qtype):
+    """fp32 tokens far outside fp16's range (|x| up to 3e7, one token tiny): the per-token
+    power-of-two scale keeps the fp16 split exact in range; values against the oracle."""
+    cols, rows = 1024, 192
+    host, w = weights(qtype, 0x68, rows, cols, N.CDNA4)
+    x = N.synth_normal_f32(0x69, 4 * cols).reshape(4, cols).copy()
+    x[0] *= 3e5
+    x[1, 5] = 3e7
+    x[2] *= 1e-6
+    xd = torch.from_numpy(x).cuda()
+    y = torch.empty((4, rows), dtype=torch.float32, device="cuda")
+    ctx.matmul(w, qtype, N.CDNA4, cols, rows, 4, xd, y)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    for t in range(4):
+        assert rel_err(got[t], O.gemv(qtype, O.ROW_MAJOR, host, cols, rows, x[t])) <= TOL32, t
