@@ -498,17 +498,19 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
     __syncthreads();
     if (!last_flag) return;
     if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // Last arrival: the parts are added in part order (deterministic).  For kparts <= 4 one
-    // round trip loads every part of one token sub-tile (4 x 32 loads per lane,
-    // unconditional: a slot past kparts re-reads part 0 and is not added); more parts go one
-    // at a time.  The accumulators are not read here (their index would be a loop variable).
+    // Last arrival: the parts are added in part order (deterministic), four parts of one token
+    // sub-tile per round trip (4 x 32 loads per lane, unconditional: a slot past kparts re-reads
+    // the last part and is not added).  A loop that loads and adds one value at a time waits for
+    // every load (each reuses the register the add just read): at 8 parts that took the Q6_K
+    // down at batch 512 from ~100 to ~520 us.  The accumulators are not read here (their index
+    // would be a loop variable).
     for (int i = 0; i < MI; ++i) {
         float sum[16][NJ];
-        if (kparts <= 4) {
+        for (uint32_t p0 = 0; p0 < kparts; p0 += 4) {
             float pv[4][16][NJ];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const uint32_t part = uint32_t(u) < kparts ? uint32_t(u) : 0u;
+                const uint32_t part = __builtin_elementwise_min(p0 + uint32_t(u), kparts - 1);
 #pragma unroll
                 for (int v = 0; v < 16; ++v)
 #pragma unroll
@@ -520,22 +522,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
             for (int v = 0; v < 16; ++v)
 #pragma unroll
                 for (int j = 0; j < NJ; ++j) {
-                    float t = pv[0][v][j];
+                    float t = p0 == 0 ? pv[0][v][j] : sum[v][j] + pv[0][v][j];
 #pragma unroll
-                    for (int u = 1; u < 4; ++u) t = uint32_t(u) < kparts ? t + pv[u][v][j] : t;
+                    for (int u = 1; u < 4; ++u) t = p0 + uint32_t(u) < kparts ? t + pv[u][v][j] : t;
                     sum[v][j] = t;
                 }
-        } else {
-            for (uint32_t part = 0; part < kparts; ++part) {
-#pragma unroll
-                for (int v = 0; v < 16; ++v)
-#pragma unroll
-                    for (int j = 0; j < NJ; ++j) {
-                        const float val = __hip_atomic_load(reinterpret_cast<float *>(pbase(part) + poff(i, v, j)),
-                                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        sum[v][j] = part == 0 ? val : sum[v][j] + val;
-                    }
-            }
         }
         write_out(i, [&](int v, int j) { return sum[v][j]; });
     }

@@ -403,6 +403,27 @@ def test_prefill_q4k_down_full_size(ctx, acc):
             assert rel_err(yy[:, r0:r0 + 128], O.gemm(N.Q4_K, O.ROW_MAJOR, ds, F, 128, B, x, 1)) <= TOL16_SAME
 
 
+@pytest.mark.parametrize("acc", [N.ACC_FP32, N.ACC_FP16], ids=["fp32acc", "fp16acc"])
+@pytest.mark.parametrize("batch", [512, 256])
+def test_prefill_q6k_down_many_parts(ctx, batch, acc):
+    """The down projection below batch 1024 splits K into 8 parts (fewer token tiles): the
+    last workgroup adds them four at a time.  128-row samples against the oracle in the same
+    mode, and the values do not depend on the part count beyond fp32 rounding (kparts 4)."""
+    D, F = 3840, 15360
+    hd, wd = weights(N.Q6_K, 67, D, F, N.CDNA4)
+    x = N.synth_normal_f16(68, batch * F).reshape(batch, F)
+    fast = acc == N.ACC_FP16
+    y = torch.empty((batch, D), dtype=torch.float32, device="cuda")
+    ctx.ffn_down(wd, N.Q6_K, N.CDNA4, F, D, batch, dev_u16(x), y, half_input=True, fast_swa=fast)
+    torch.cuda.synchronize()
+    yy = y.cpu().numpy()
+    assert np.isfinite(yy).all()
+    for r0 in (0, D - 128):
+        ds = _row_slice(hd, N.Q6_K, F, r0, 128)
+        ref = O.gemm(N.Q6_K, O.ROW_MAJOR, ds, F, 128, batch, x, 1 if fast else 0)
+        assert rel_err(yy[:, r0:r0 + 128], ref) <= (TOL16_SAME if fast else TOL32)
+
+
 # ---- device layout conversion and argument errors -------------------------------
 
 @pytest.mark.parametrize("qtype", [N.Q4_K, N.Q6_K], ids=["q4k", "q6k"])
