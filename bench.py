@@ -496,10 +496,11 @@ class Bench:
     def pmc_driver(self):
         """The launch sequence the rocprofv3 --pmc passes read: every prefill GEMM instance at
         batch 1024 (gate/up pair, Q6_K and Q4_K down; FP32 then FP16 mode), the decode GEMVs
-        (config 0's Q4_K, config 1's Q6_K down, the gate/up pair), --steps launches each, then
-        three copies of a 256 MiB buffer, the copy of known size that scales FETCH_SIZE and
-        WRITE_SIZE.  Weights rotate over two copies so a launch cannot find the previous one's
-        weights in the Infinity Cache."""
+        (config 0's Q4_K, config 1's Q6_K down, the gate/up pair) and the batch-4 kernels (the
+        lm-head, the gate/up pair, the Q6_K down), --steps launches each, then three copies of a
+        256 MiB buffer, the copy of known size that scales FETCH_SIZE and WRITE_SIZE.  Weights
+        rotate over two copies so a launch cannot find the previous one's weights in the
+        Infinity Cache (the lm-head, 826 MB, cannot stay there either)."""
         N, torch, ctx, n = self.N, self.torch, self.ctx, self.args.steps
         g = [self.weights(Q4, 0x90 + i, F, D) for i in range(2)]
         u = [self.weights(Q4, 0x92 + i, F, D) for i in range(2)]
@@ -528,10 +529,24 @@ class Bench:
             ctx.matmul(d6[i % 2], Q6, N.CDNA4, F, D, 1, hd, yd2)
         for i in range(n):
             ctx.gate_up_geglu_decode(g[i % 2], u[i % 2], N.CDNA4, D, F, xd, hdo)
+        # batch 4 (MTP verification) on the matrix cores: the lm-head, the gate/up pair, the Q6_K down
+        lm = self.weights(Q6, 0x1B, V, D)
+        x4, xh4, hh4 = self.f32(0xB4, 4 * D), self.f16(0xB6, 4 * D), self.f16(0xB8, 4 * F)
+        lg = torch.empty((4, V), dtype=torch.float32, device="cuda")
+        h4 = torch.empty((4, F), dtype=torch.int16, device="cuda")
+        y4 = torch.empty((4, D), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        for i in range(n):
+            ctx.matmul(lm, Q6, N.CDNA4, D, V, 4, x4, lg)
+        for i in range(n):
+            ctx.gate_up_geglu(g[i % 2], u[i % 2], N.CDNA4, D, F, 4, xh4, h4)
+        for i in range(n):
+            ctx.ffn_down(d6[i % 2], Q6, N.CDNA4, F, D, 4, hh4, y4, True, False)
         for _ in range(3):
             b.copy_(a)
         torch.cuda.synchronize()
-        log(f"pmc driver: {n} launches of each prefill GEMM (both modes) and decode GEMV, 3 x 256 MiB copies")
+        log(f"pmc driver: {n} launches of each prefill GEMM (both modes), decode GEMV and batch-4 kernel, "
+            f"3 x 256 MiB copies")
 
     def lmhead_only(self):
         N, torch, ctx = self.N, self.torch, self.ctx

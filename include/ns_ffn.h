@@ -45,10 +45,14 @@ enum { NS_TYPE_Q4_K = 12, NS_TYPE_Q6_K = 14 };
 enum { NS_LAYOUT_ROW_MAJOR = 0, NS_LAYOUT_NSMFFN = 1, NS_LAYOUT_CDNA4 = 2 };
 
 /* Accumulation mode of the prefill GEMMs (mm:565 `fast_swa_ffn`).
- *   FP32  fp32 accumulation (the 8 global layers, and every layer with --exact-ffn).
- *   FP16  the local-layer mode: the running fp32 sum is rounded to fp16
+ *   FP32  fp32 accumulation of exact products (the 8 global layers, and every
+ *         layer with --exact-ffn).
+ *   FP16  the local-layer mode: the weights enter as fp16 tiles, the reference's
+ *         half(d*sc*q - dmin*m) / half(d*sc*(v-32)) times a power of two per
+ *         weight row (which keeps small blocks out of fp16's subnormals); the
+ *         products are summed in fp32, and each output is rounded once to fp16
  *         precision (11 significant bits, round to nearest even, fp32 exponent
- *         range) at every 256-wide super-block boundary. */
+ *         range), whatever the summation order or split. */
 enum { NS_ACC_FP32 = 0, NS_ACC_FP16 = 1 };
 
 enum {
@@ -94,7 +98,8 @@ int ns_ctx_set_tuning(ns_ctx *ctx, const char *key, int value);
 /* NativeMetalEngine::matmul (mm:269-275): out = in . W^T for `batch` tokens.
  *   batch == 1, fp32 input      -> dequant-fused GEMV (decode; lm-head with ROW_MAJOR or CDNA4).
  *   batch 2-4, fp32 or fp16     -> small-batch GEMV streaming the weights once for all tokens
- *                                  (gemma_q4k/q6k_mm_fast[_f16][_metal], metal:125-177, mm:273).
+ *                                  (gemma_q4k/q6k_mm_fast[_f16][_metal], metal:125-177, mm:273);
+ *                                  on the matrix cores for the CDNA4 layout, FP32 accumulation.
  *   batch  > 4, half_input != 0 -> dequant-into-LDS MFMA GEMM, FP32 accumulation (any layout:
  *                                  the reference's swizzled row-major kernels, metal:263-301,
  *                                  432-478, serve attention tensors that stay row-major).
@@ -141,7 +146,7 @@ int ns_ffn_down(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols,
                 void *stream);
 
 /* Bit-exact check hook: dequantise rows [row0, row0+nrows) to fp32 (quant.cpp:20
- * values) and/or fp16 (RNE of that fp32, the value the GEMM tiles hold).
+ * values) and/or fp16 (RNE of that fp32).
  * Either output may be NULL.  Outputs are [nrows][cols]. */
 int ns_dequant(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, uint32_t rows,
                uint32_t row0, uint32_t nrows, float *out_f32, uint16_t *out_f16, void *stream);

@@ -13,7 +13,7 @@
 // VALU work is the unpack and that FMA.
 //
 // Work split.  One workgroup = 4 waves, one wave per SIMD, one workgroup per CU
-// (96 KiB of LDS).  A workgroup computes 256 tokens x 256 B columns; each wave
+// (128 KiB of LDS).  A workgroup computes 256 tokens x 256 B columns; each wave
 // owns all 256 tokens (8 MFMA tiles of v_mfma_f32_32x32x16_f16) and 64 columns
 // (2 tiles): for the gate/up pair, 32 gate rows and the same 32 up rows, so
 // GeGLU runs in registers.  The 256 fp32 accumulators of a wave live in AGPRs.
@@ -22,7 +22,7 @@
 // which in the CDNA4 layout are 8 contiguous bytes of that row's 16-byte chunk
 // (lanes 0-31 and 32-63 take the two halves, so one load instruction reads
 // 512 contiguous bytes).  Each decoded fragment feeds 8 MFMAs.  x streams into
-// LDS by buffer_load ... lds (three 32 KiB buffers, one barrier per 64-wide k
+// LDS by buffer_load ... lds (four 32 KiB buffers, one barrier per 64-wide k
 // step) and each A fragment (ds_read_b128) feeds 2 MFMAs.
 //
 // Row scales: every wave first reads the d (and dmin) of all super-blocks of its

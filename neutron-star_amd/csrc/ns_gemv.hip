@@ -1232,7 +1232,7 @@ hipError_t launch_gemv(int type, int layout, const uint8_t *w, const uint8_t *up
 
 void gemv_mt_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, bool pair, uint32_t batch, bool xh,
                             const Tuning &t, size_t *partial_floats, size_t *counters) {
-    if (gemv_mfma_eligible(layout, pair, xh, t)) return gemv_mfma_workspace_need(cols, rows, pair, t, partial_floats, counters);
+    if (gemv_mfma_eligible(layout, pair, xh, batch, t)) return gemv_mfma_workspace_need(cols, rows, pair, t, partial_floats, counters);
     const uint32_t nt = mt_tokens(batch, xh);
     const GemvPlan p = dispatch_mt(type, layout, pair, nt, xh, [&](auto m) { return decltype(m)::plan(cols, rows, t); });
     *partial_floats = size_t(p.G) * 2 * 64 * (pair ? 2 : 1) * nt;
@@ -1243,7 +1243,7 @@ hipError_t launch_gemv_mt(int type, int layout, const uint8_t *w, const uint8_t 
                           uint32_t batch, void *out, uint32_t cols, uint32_t rows, const Workspace &ws,
                           hipStream_t stream) {
     const bool pair = up != nullptr;
-    if (gemv_mfma_eligible(layout, pair, xh, ws.tune))
+    if (gemv_mfma_eligible(layout, pair, xh, batch, ws.tune))
         return launch_gemv_mfma(type, w, up, x, xh, batch, out, cols, rows, ws, stream);
     return dispatch_mt(type, layout, pair, mt_tokens(batch, xh), xh, [&](auto m) {
         using M = decltype(m);

@@ -67,7 +67,7 @@ hipError_t launch_gemv_mt(int type, int layout, const uint8_t *w, const uint8_t 
                           hipStream_t stream);
 // Batch 1-4 on the matrix cores (ns_gemv_mfma.hip), CDNA4 layout; launch_gemv_mt routes there
 // when gemv_mfma_eligible.
-bool gemv_mfma_eligible(int layout, bool pair, bool xh, const Tuning &t);
+bool gemv_mfma_eligible(int layout, bool pair, bool xh, uint32_t batch, const Tuning &t);
 void gemv_mfma_workspace_need(uint32_t cols, uint32_t rows, bool pair, const Tuning &t, size_t *partial_floats,
                               size_t *counters);
 hipError_t launch_gemv_mfma(int type, const uint8_t *w, const uint8_t *up, const void *x, bool xh, uint32_t batch,
