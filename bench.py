@@ -21,11 +21,15 @@ The CPU leg (skipped by --no-cpu) times the oracle on the host cores: config 1 a
 line's cpu_baseline, and beside configs 0, 2, 3 (both modes) and 4's decode step in
 "extra" (cpu_* keys), each on a bounded sample named in cpu_samples.
 
-usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+Before the W warm-up steps, config-1 steps run untimed for --ramp-ms of wall time (default 300),
+so that the GPU's clock has settled whatever W is.
+
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--ramp-ms MS] [--no-cpu]
                        [--only all|headline|lmhead|pmc|prefill|stack|smallbatch]
   --only lmhead runs just the lm-head GEMV (K launches) and a 256 MiB device copy
   of known size: the driver for the rocprofv3 --pmc traffic runs.
-  --only pmc does the same for the prefill GEMMs and the small decode GEMVs.
+  --only pmc does the same for the prefill GEMMs, the small decode GEMVs and the batch-4
+  kernels.
 """
 import argparse
 import json
@@ -217,6 +221,17 @@ class Bench:
         # leaves the stream idle ~4.5 us, so only every EVERY-th step is bracketed:
         # the timing covers steps/EVERY launches and the other steps run bare.
         EVERY = 5
+        # Clock ramp, before the W warm-up steps and not counted as steps: the first ~100
+        # config-1 steps after start-up run ~10% slower (153.9 against 139.4 us per step),
+        # the GPU's clock and power state settling.  Config-1 steps are repeated untimed
+        # until --ramp-ms of wall time has passed, so the timed window sees the steady state
+        # whatever --warmup the caller passes.
+        t_ramp, i = time.perf_counter(), 0
+        while (time.perf_counter() - t_ramp) * 1e3 < args.ramp_ms:
+            for _ in range(50):
+                step(i)
+                i += 1
+            torch.cuda.synchronize()
         for i in range(args.warmup):
             step(i)
         torch.cuda.synchronize()
@@ -572,6 +587,8 @@ def main():
     # 200 untimed steps (~30 ms): the first ~100 config-1 steps after start-up run ~10% slower
     # (clock ramp and the first touch of the 16 down copies), which 5 steps left in the timed window
     ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--ramp-ms", type=float, default=300.0,
+                    help="untimed config-1 steps before the warm-up steps, in ms of wall time (clock ramp)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--quick", action="store_true", help="same as --only headline")
     ap.add_argument("--only", default="all",
