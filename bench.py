@@ -24,7 +24,7 @@ line's cpu_baseline, and beside configs 0, 2, 3 (both modes) and 4's decode step
 Before the W warm-up steps, config-1 steps run untimed for --ramp-ms of wall time (default 300),
 so that the GPU's clock has settled whatever W is.
 
-usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--ramp-ms MS] [--no-cpu]
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--ramp-ms MS] [--no-cpu] [--tune KEY=VALUE]
                        [--only all|headline|lmhead|pmc|prefill|stack|smallbatch]
   --only lmhead runs just the lm-head GEMV (K launches) and a 256 MiB device copy
   of known size: the driver for the rocprofv3 --pmc traffic runs.
@@ -159,6 +159,9 @@ class Bench:
         assert torch.cuda.is_available(), "no GPU visible"
         torch.cuda.set_device(0)
         self.ctx = N.Context(0)
+        for kv in args.tune:  # kernel-choice overrides for A/B runs (ns_ctx_set_tuning)
+            key, val = kv.split("=")
+            self.ctx.set_tuning(key, int(val))
         self.stream = torch.cuda.current_stream()
         self.extra = {}
         self._stage = None
@@ -475,8 +478,9 @@ class Bench:
         def decode_step(_i=0):
             inp = xd
             for l, lay in enumerate(layers):
-                ctx.rms_gate_up_geglu_decode(lay["gate"], lay["up"], N.CDNA4, D, F, inp, norm_w[l], EPS, h)
-                ctx.ffn_down(lay["down"], down_type(l), N.CDNA4, F, D, 1, h, y, False, False)
+                # rms (mm:563), gate/up + GeGLU and down (mm:571-573): one launch per layer
+                ctx.ffn_block_decode(lay["gate"], lay["up"], lay["down"], down_type(l), N.CDNA4, D, F, inp, h, y,
+                                     norm_weight=norm_w[l], eps=EPS)
                 inp = y
             ctx.rmsnorm(y, norm_w[NLAYERS], 1, D, EPS, xs)  # the output norm ahead of the lm-head (mm:576)
             ctx.matmul(self.lm, Q6, N.CDNA4, D, V, 1, xs, logits)
@@ -591,6 +595,8 @@ def main():
                     help="untimed config-1 steps before the warm-up steps, in ms of wall time (clock ramp)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--quick", action="store_true", help="same as --only headline")
+    ap.add_argument("--tune", action="append", default=[], metavar="KEY=VALUE",
+                    help="override one kernel choice (ns_ctx_set_tuning key), for A/B runs; repeatable")
     ap.add_argument("--only", default="all",
                     choices=["all", "headline", "lmhead", "pmc", "prefill", "stack", "smallbatch"])
     args = ap.parse_args()

@@ -91,8 +91,10 @@ int ns_ctx_workspace_bytes(const ns_ctx *ctx, uint64_t *bytes);
  * "gemm_q4_reg" (0: the LDS-tile Q4_K GEMM), "mt_mfma" (0: batch 1-4 of the
  * CDNA4 layout on the VALU kernel instead of the matrix cores), "mt_parts" /
  * "mt_slabs" / "mt_spw" (> 0: that MFMA kernel's column parts per workgroup,
- * slabs per workgroup, super-blocks per wave).  Results stay within the same
- * tolerances; engines leave the defaults. */
+ * slabs per workgroup, super-blocks per wave), "block_fused" (0: the decode
+ * FFN block as two launches), "block_spin" (> 0: the one-launch block's bound on
+ * a wait, in polls; tests shorten it to exercise the bound).  Results stay within
+ * the same tolerances; engines leave the defaults. */
 int ns_ctx_set_tuning(ns_ctx *ctx, const char *key, int value);
 
 /* NativeMetalEngine::matmul (mm:269-275): out = in . W^T for `batch` tokens.
@@ -177,6 +179,22 @@ int ns_rmsnorm_add_then(ns_ctx *ctx, const float *x, const float *weight, const 
 int ns_rms_gate_up_geglu_decode(ns_ctx *ctx, const void *wg, const void *wu, int layout, uint32_t cols,
                                 uint32_t rows, const float *x, const float *norm_weight, float eps, float *h,
                                 void *stream);
+
+/* The decode FFN block (mm:571-573: gate_up_geglu_decode, then ffn_down) in one launch
+ * where the shapes allow it (CDNA4 layout, (ffn/256) a multiple of (cols/256) <= 16, as
+ * the model's 3840 / 15360 are), else as those two launches.  No single counterpart in
+ * the reference: it is the engine's pair of calls.  h = gelu(Wg.n) * (Wu.n), y = Wd.h,
+ * with n = x, or with norm_weight non-null n = (x * r) * norm_weight, r = 1/sqrt(mean(x^2)
+ * + eps) (the rms ahead of the FFN, mm:563, as ns_rms_gate_up_geglu_decode).  x fp32
+ * [cols], h fp32 [ffn] (written), y fp32 [cols].  At the model's shape the results equal
+ * the two launches bit for bit (the same per-row order), elsewhere within their FP32
+ * tolerance.  y may alias x; h may not overlap either.  x, norm_weight and h 16-byte
+ * aligned.  Calls that overlap on one context race (the launch counts its workgroups in
+ * the context's workspace).  The one launch's down workgroups wait for the gate/up rows
+ * they read, with a bound of seconds: rows of y whose wait ran out are NaN. */
+int ns_ffn_block_decode(ns_ctx *ctx, const void *wg, const void *wu, const void *wd, int down_type, int layout,
+                        uint32_t cols, uint32_t ffn, const float *x, const float *norm_weight, float eps, float *h,
+                        float *y, void *stream);
 
 /* gemma_q6k_embedding (metal:503-505; the token embedding at mm:310, scale = sqrt(3840)):
  * out[t][i] = scale * W[ids[t]][i], fp32 [batch][cols], each value as quant.cpp computes it.

@@ -121,6 +121,9 @@ void model_workspace_need(const Tuning &t, size_t *floats, size_t *counters) {
                 take(f, c);
             }
         }
+    size_t f = 0, c = 0;
+    block_decode_workspace_need(3840, 15360, &f, &c);
+    take(f, c);
     *floats = pf;
     *counters = nc;
 }
@@ -205,6 +208,8 @@ extern "C" int ns_ctx_set_tuning(ns_ctx *ctx, const char *key, int value) {
     else if (k == "mt_parts") t.mt_parts = value;
     else if (k == "mt_slabs") t.mt_slabs = value;
     else if (k == "mt_spw") t.mt_spw = value;
+    else if (k == "block_fused") t.block_fused = value;
+    else if (k == "block_spin") t.block_spin = value;
     else return fail(NS_ERR_ARG, "ns_ctx_set_tuning: unknown key " + k);
     return NS_OK;
 }
@@ -364,6 +369,42 @@ extern "C" int ns_rms_gate_up_geglu_decode(ns_ctx *ctx, const void *wg, const vo
     np.wb = norm_weight;
     np.eps = eps;
     return rms_gate_up(ctx, "ns_rms_gate_up_geglu_decode", wg, wu, layout, cols, rows, np, h, stream);
+}
+
+extern "C" int ns_ffn_block_decode(ns_ctx *ctx, const void *wg, const void *wu, const void *wd, int down_type,
+                                   int layout, uint32_t cols, uint32_t ffn, const float *x, const float *norm_weight,
+                                   float eps, float *h, float *y, void *stream) {
+    const char *fn = "ns_ffn_block_decode";
+    if (!ctx) return fail(NS_ERR_ARG, "ns_ffn_block_decode: null context");
+    if (int rc = check_tensor(fn, wg, Q4_K, layout, cols, ffn)) return rc;
+    if (int rc = check_tensor(fn, wu, Q4_K, layout, cols, ffn)) return rc;
+    if (int rc = check_tensor(fn, wd, down_type, layout, ffn, cols)) return rc;
+    if (!x || !h || !y) return fail(NS_ERR_ARG, "ns_ffn_block_decode: null input/output");
+    const auto overlap = [](const void *a, size_t na, const void *b, size_t nb) {
+        const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+        return pa < pb + nb && pb < pa + na;
+    };
+    if (overlap(h, ffn * 4, x, cols * 4)) return fail(NS_ERR_ARG, "ns_ffn_block_decode: h overlaps x");
+    if (overlap(h, ffn * 4, y, cols * 4)) return fail(NS_ERR_ARG, "ns_ffn_block_decode: h overlaps y");
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(norm_weight) | reinterpret_cast<uintptr_t>(h)) % 16)
+        return fail(NS_ERR_ARG, "ns_ffn_block_decode: x, norm_weight and h must be 16-byte aligned");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (ctx->ws.tune.block_fused != 0 && block_decode_supported(layout, down_type, norm_weight != nullptr, cols, ffn)) {
+        size_t pf = 0, nc = 0;
+        block_decode_workspace_need(cols, ffn, &pf, &nc);
+        if (int rc = ensure_ws(ctx, pf, nc, s)) return rc;
+        const hipError_t e = launch_block_decode(down_type, static_cast<const uint8_t *>(wg),
+                                                 static_cast<const uint8_t *>(wu), static_cast<const uint8_t *>(wd), x,
+                                                 norm_weight, eps, h, y, cols, ffn, ctx->ws, s);
+        return e == hipSuccess ? NS_OK : hip_fail(e, fn);
+    }
+    // two launches (mm:571-573): gate/up + GeGLU (with the norm when given), then down
+    if (norm_weight) {
+        if (int rc = ns_rms_gate_up_geglu_decode(ctx, wg, wu, layout, cols, ffn, x, norm_weight, eps, h, stream)) return rc;
+    } else if (int rc = ns_gate_up_geglu_decode(ctx, wg, wu, layout, cols, ffn, x, h, stream)) {
+        return rc;
+    }
+    return ns_matmul(ctx, wd, down_type, layout, ffn, cols, 1, h, 0, y, stream);
 }
 
 extern "C" int ns_embedding(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, uint32_t rows,

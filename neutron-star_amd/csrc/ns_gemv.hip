@@ -1212,6 +1212,201 @@ auto dispatch_mt(int type, int layout, bool pair, uint32_t nt, bool xh, Fn &&fn)
 // x in, and the spilled instance is slower than the four-token one (MI355X).
 uint32_t mt_tokens(uint32_t batch, bool xh) { return xh && batch <= 2 ? 2u : 4u; }
 
+// ---- the decode FFN block in one launch (mm:571-573), CDNA4 layout -----------------
+//
+// gate/up + GeGLU writes h, the down projection reads it.  As two launches the down
+// projection's weights, which do not depend on h, start streaming only after the last
+// gate/up workgroup has drained, and each launch pays its own ramp and tail.  Here one grid
+// of NG = F/64 workgroups of W = D/256 waves does both; workgroup g:
+//   1. gate/up slab g, one super-block per wave (the whole-slab grid of the decode GEMV:
+//      the pair's dot products, optionally with the RMSNorm of x folded in, the waves' parts
+//      added in LDS in wave order), h = gelu(g)*u stored with agent-scope stores; once they
+//      are acknowledged, one arrival on ready[kq], kq = g / DS (DS = D/64 = 4W), the column
+//      part of the down projection that these 64 rows of h feed;
+//   2. as soon as its gate/up weights are consumed, each wave requests its down weights
+//      (wave 0 after its arrival): the down projection's (slab g % DS, column part kq), one
+//      super-block per wave, so the down weights stream while other workgroups still finish
+//      their gate/up slabs;
+//   3. waits until ready[kq] counts the DS gate/up slabs of part kq (workgroups kq*DS ..
+//      kq*DS + DS-1), reads h with agent-scope loads, and finishes as the decode GEMV's
+//      k-workgroups-per-slab plan does: the KQ parts of one slab added in part order by the
+//      last to arrive.
+// NG = DS * KQ always (F/64 = (D/64) * (F/D)), so every workgroup has exactly one task of
+// each kind.  The wait in 3 needs the workgroups it waits on to run: the host launches this
+// kernel only when the whole grid fits on the device at once (NG <= CUs x resident
+// workgroups per CU), so every workgroup is dispatched whatever else runs on the device:
+// work of other kernels ends without waiting on this one and frees its CUs.  The wait is also
+// bounded: a workgroup whose spin limit runs out records it in status and goes on, so every
+// wave exits, and the slabs finished after that are written as NaN (the limit is seconds
+// long).  The last slab to finish clears the counters for the next launch.  Per row and part
+// the arithmetic and its order are those of the two launches (gemv_kernel's whole-slab
+// gate/up and its k-workgroups-per-slab down), so the results are the same bit for bit.
+constexpr uint32_t kBlockMaxW = 16;
+constexpr uint32_t kCtrStride = 32;  // one counter per 128-byte line
+
+// signal fences keep the compiler from moving memory operations across the barrier; the
+// barrier itself does not wait for this wave's global loads in flight
+__device__ __forceinline__ void lds_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// 4 waves per SIMD (at most 128 VGPRs) is the occupancy the grid is sized for; without the
+// bound the compiler trades the loads in flight for registers
+template <int DTYPE, bool NORM>
+__global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) void block_decode_kernel(
+    const uint8_t *__restrict__ wg, const uint8_t *__restrict__ wu, const uint8_t *__restrict__ wd,
+    const float *__restrict__ x, const float *__restrict__ normw, float eps, float *__restrict__ h,
+    float *__restrict__ y, uint32_t D, uint32_t F, float *__restrict__ partial, uint32_t *__restrict__ ctr,
+    uint32_t spin_limit) {
+    __shared__ __attribute__((aligned(16))) float lds_x[kBlockMaxW * kQK];
+    __shared__ float lds_part[kBlockMaxW][2][64];
+    __shared__ float lds_sum[kBlockMaxW];
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nbg = D / kQK, nbd = F / kQK, KQ = nbd / nbg, DS = D / kRowTile, W = nbg;
+    const uint32_t g = blockIdx.x, kq = g / DS, dslab = g - kq * DS;
+    // ctr: slabs_done, status, then ready[KQ] and arrive[DS], each on a line of its own
+    uint32_t *slabs_done = ctr, *status = ctr + 1, *ready = ctr + kCtrStride;
+    uint32_t *arrive = ctr + kCtrStride * (1 + KQ);
+    float *xw = lds_x + wave * kQK;  // this wave's 256 inputs
+
+    // ---- 1. gate/up slab g, super-block `wave` ----
+    {
+        u32x4 c[2][kQ4Chunks];
+        const float4 xv = reinterpret_cast<const float4 *>(x + size_t(wave) * kQK)[lane];
+        float4 wv{1.f, 1.f, 1.f, 1.f};
+        if constexpr (NORM) wv = reinterpret_cast<const float4 *>(normw + size_t(wave) * kQK)[lane];
+        q4_load<CDNA4>(wg, lane, 0, g, wave, nbg, c[0]);
+        q4_load<CDNA4>(wu, lane, 0, g, wave, nbg, c[1]);
+        const float4 xin = NORM ? float4{xv.x * wv.x, xv.y * wv.y, xv.z * wv.z, xv.w * wv.w} : xv;
+        reinterpret_cast<float4 *>(xw)[lane] = xin;
+        if constexpr (NORM) {
+            float sq = sumsq4(xv, 0.f);
+            for (int m = 32; m >= 1; m >>= 1) sq += __shfl_xor(sq, m);
+            if (lane == 0) lds_sum[wave] = sq;
+        }
+        float xs[8], r[2];
+        group_sums_of<32>(xin, xs);
+        q4_dot<2>(c, xw, xs, r);
+        lds_part[wave][0][lane] = r[0];
+        lds_part[wave][1][lane] = r[1];
+    }
+    // ---- 2. this wave's down weights: slab dslab, part kq, super-block kq*W + wave ----
+    // (wave 0 requests them after its arrival below: the arrival waits for all of wave 0's
+    // memory operations to complete)
+    const uint32_t b = kq * nbg + wave;
+    u32x4 c[DTYPE == Q4_K ? kQ4Chunks : kQ6Chunks];
+    uint32_t dbits = 0;
+    const auto load_down = [&] {
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        if constexpr (DTYPE == Q4_K) q4_load<CDNA4>(wd, lane, 0, dslab, b, nbd, c);
+        else q6_load<CDNA4>(wd, lane, 0, dslab, b, nbd, c, dbits);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    };
+    if (wave != 0) load_down();
+    lds_barrier();
+    if (wave == 0) {
+        float gs = 0.f, us = 0.f;
+        for (uint32_t v = 0; v < W; ++v) {
+            gs += lds_part[v][0][lane];
+            us += lds_part[v][1][lane];
+        }
+        if constexpr (NORM) {
+            float ts = 0.f;
+            for (uint32_t v = 0; v < W; ++v) ts += lds_sum[v];
+            const float rs = rms_factor(ts, D, eps);
+            gs *= rs;
+            us *= rs;
+        }
+        __hip_atomic_store(&h[g * kRowTile + lane], gelu_tanh(gs) * us, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // the stores are acknowledged before the arrival is counted
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        if (lane == 0) __hip_atomic_fetch_add(&ready[kq * kCtrStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        load_down();
+        // ---- 3. wait for the DS gate/up slabs of part kq ----
+        if (lane == 0) {
+            uint32_t it = 0;
+            while (__hip_atomic_load(&ready[kq * kCtrStride], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < DS) {
+                __builtin_amdgcn_s_sleep(1);
+                if (++it >= spin_limit) {
+                    __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+            }
+        }
+    }
+    // wave 0's reads of lds_part end before any wave writes it again below
+    lds_barrier();
+    const float *hb = h + size_t(b) * kQK + 4 * lane;
+    const float4 hv{__hip_atomic_load(hb + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                    __hip_atomic_load(hb + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                    __hip_atomic_load(hb + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                    __hip_atomic_load(hb + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)};
+    reinterpret_cast<float4 *>(xw)[lane] = hv;
+    float acc;
+    if constexpr (DTYPE == Q4_K) {
+        const u32x4(&cc)[1][kQ4Chunks] = reinterpret_cast<const u32x4(&)[1][kQ4Chunks]>(c);
+        float xs[8], r[1];
+        group_sums_of<32>(hv, xs);
+        q4_dot<1>(cc, xw, xs, r);
+        acc = r[0];
+    } else {
+        float xs[16];
+        group_sums_of<16>(hv, xs);
+        acc = q6_dot(c, dbits, xw, xs);
+    }
+    lds_part[wave][0][lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+        float r0 = 0.f;
+        for (uint32_t v = 0; v < W; ++v) r0 += lds_part[v][0][lane];
+        float *dst = partial + (size_t(dslab) * KQ + kq) * 64;
+        __hip_atomic_store(&dst[lane], r0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        uint32_t prev = 0;
+        if (lane == 0)
+            prev = __hip_atomic_fetch_add(&arrive[dslab * kCtrStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        prev = __builtin_amdgcn_readfirstlane(__shfl(prev, 0));
+        if (prev == KQ - 1) {
+            // the column parts of the slab, loaded 16 at a time and added in part order
+            float sum = 0.f;
+            const float *src = partial + size_t(dslab) * KQ * 64;
+            for (uint32_t q0 = 0; q0 < KQ; q0 += 16) {
+                float v[16];
+#pragma unroll
+                for (uint32_t j = 0; j < 16; ++j)
+                    v[j] = __hip_atomic_load(&src[__builtin_elementwise_min(q0 + j, KQ - 1) * 64 + lane],
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                for (uint32_t j = 0; j < 16; ++j)
+                    if (q0 + j < KQ) sum += v[j];
+            }
+            // a part that stopped waiting read h too early: the slab is not a result
+            const bool late = __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+            y[dslab * kRowTile + lane] = late ? __builtin_nanf("") : sum;
+            if (lane == 0) {
+                __hip_atomic_store(&arrive[dslab * kCtrStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                // every workgroup has arrived once the last slab is done: nothing reads
+                // ready or status any more in this launch
+                const uint32_t done = __hip_atomic_fetch_add(slabs_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (done == DS - 1) {
+                    __hip_atomic_store(slabs_done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(status, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    for (uint32_t k = 0; k < KQ; ++k)
+                        __hip_atomic_store(&ready[k * kCtrStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        }
+    }
+}
+
 }  // namespace
 
 void gemv_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, bool pair, const Tuning &t,
@@ -1252,6 +1447,65 @@ hipError_t launch_gemv_mt(int type, int layout, const uint8_t *w, const uint8_t 
                                                                ws.partial, ws.counters);
         return hipGetLastError();
     });
+}
+
+
+template <int DTYPE, bool NORM>
+constexpr auto block_kernel_of() {
+    return &block_decode_kernel<DTYPE, NORM>;
+}
+
+// Workgroups of nbg waves of one instance that a CU holds at once, per device.
+template <int DTYPE, bool NORM>
+int block_wgs_per_cu(uint32_t nbg) {
+    static int cache[64][kBlockMaxW + 1] = {};
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    int &w = cache[dev & 63][nbg];
+    if (w == 0) {
+        int wgs = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&wgs, block_kernel_of<DTYPE, NORM>(), int(nbg) * 64, 0) !=
+                hipSuccess || wgs <= 0)
+            wgs = -1;  // unknown: never taken as room
+        w = wgs;
+    }
+    return w;
+}
+
+bool block_decode_supported(int layout, int down_type, bool norm, uint32_t cols, uint32_t ffn) {
+    const uint32_t nbg = cols / kQK, nbd = ffn / kQK;
+    if (!(layout == CDNA4 && cols % kQK == 0 && ffn % kQK == 0 && nbg >= 1 && nbg <= kBlockMaxW && nbd % nbg == 0))
+        return false;
+    // the whole grid (ffn/64 workgroups) must fit on the device at once
+    const int per_cu = down_type == Q4_K ? (norm ? block_wgs_per_cu<Q4_K, true>(nbg) : block_wgs_per_cu<Q4_K, false>(nbg))
+                                         : (norm ? block_wgs_per_cu<Q6_K, true>(nbg) : block_wgs_per_cu<Q6_K, false>(nbg));
+    return per_cu > 0 && uint64_t(ffn / kRowTile) <= uint64_t(per_cu) * uint64_t(device_shape().cus);
+}
+
+void block_decode_workspace_need(uint32_t cols, uint32_t ffn, size_t *partial_floats, size_t *counters) {
+    const uint32_t KQ = (ffn / kQK) / (cols / kQK), DS = cols / kRowTile;
+    *partial_floats = size_t(DS) * KQ * 64;         // the down projection's column parts
+    *counters = size_t(kCtrStride) * (1 + KQ + DS);  // slabs_done, status; ready[KQ]; arrive[DS]
+}
+
+hipError_t launch_block_decode(int down_type, const uint8_t *wg, const uint8_t *wu, const uint8_t *wd, const float *x,
+                               const float *normw, float eps, float *h, float *y, uint32_t cols, uint32_t ffn,
+                               const Workspace &ws, hipStream_t stream) {
+    if (!block_decode_supported(CDNA4, down_type, normw != nullptr, cols, ffn)) return hipErrorInvalidValue;
+    size_t pf = 0, nc = 0;
+    block_decode_workspace_need(cols, ffn, &pf, &nc);
+    if (ws.partial_floats < pf || ws.counter_count < nc) return hipErrorInvalidValue;
+    // 2^22 polls, each an L2 round trip plus s_sleep 1: seconds
+    const uint32_t spin = ws.tune.block_spin > 0 ? uint32_t(ws.tune.block_spin) : 1u << 22;
+    const dim3 g(ffn / kRowTile), blk((cols / kQK) * 64);
+    if (down_type == Q4_K) {
+        if (normw) block_decode_kernel<Q4_K, true><<<g, blk, 0, stream>>>(wg, wu, wd, x, normw, eps, h, y, cols, ffn, ws.partial, ws.counters, spin);
+        else block_decode_kernel<Q4_K, false><<<g, blk, 0, stream>>>(wg, wu, wd, x, normw, eps, h, y, cols, ffn, ws.partial, ws.counters, spin);
+    } else {
+        if (normw) block_decode_kernel<Q6_K, true><<<g, blk, 0, stream>>>(wg, wu, wd, x, normw, eps, h, y, cols, ffn, ws.partial, ws.counters, spin);
+        else block_decode_kernel<Q6_K, false><<<g, blk, 0, stream>>>(wg, wu, wd, x, normw, eps, h, y, cols, ffn, ws.partial, ws.counters, spin);
+    }
+    return hipGetLastError();
 }
 
 }  // namespace ns

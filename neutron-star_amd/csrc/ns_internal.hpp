@@ -26,6 +26,8 @@ struct Tuning {
     int mt_parts = 0;     // > 0: the batch 1-4 MFMA kernel's column parts per workgroup
     int mt_slabs = 0;     // > 0: its slabs per workgroup (when the columns are not split)
     int mt_spw = 0;       // > 0: its super-blocks per wave (more workgroups per slab)
+    int block_fused = 1;  // 0: the decode FFN block as two launches instead of one
+    int block_spin = 0;   // > 0: that launch's bound on a down workgroup's wait (polls)
 };
 
 // Workspace owned by ns_ctx: fp32 partial sums and per-slab arrival counters
@@ -65,6 +67,15 @@ void gemv_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, boo
 hipError_t launch_gemv_mt(int type, int layout, const uint8_t *w, const uint8_t *up, const void *x, bool xh,
                           uint32_t batch, void *out, uint32_t cols, uint32_t rows, const Workspace &ws,
                           hipStream_t stream);
+// The decode FFN block in one launch (gate/up + GeGLU into h, then down into y), CDNA4
+// layout, shapes with (ffn/256) a multiple of (cols/256) <= 16.  normw non-null folds the
+// RMSNorm of x (weight normw, eps) into the gate/up dot products.  y may alias x; h may not.
+bool block_decode_supported(int layout, int down_type, bool norm, uint32_t cols, uint32_t ffn);
+void block_decode_workspace_need(uint32_t cols, uint32_t ffn, size_t *partial_floats, size_t *counters);
+hipError_t launch_block_decode(int down_type, const uint8_t *wg, const uint8_t *wu, const uint8_t *wd, const float *x,
+                               const float *normw, float eps, float *h, float *y, uint32_t cols, uint32_t ffn,
+                               const Workspace &ws, hipStream_t stream);
+
 // Batch 1-4 on the matrix cores (ns_gemv_mfma.hip), CDNA4 layout; launch_gemv_mt routes there
 // when gemv_mfma_eligible.
 bool gemv_mfma_eligible(int layout, bool pair, bool xh, uint32_t batch, const Tuning &t);

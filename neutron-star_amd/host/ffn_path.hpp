@@ -160,6 +160,11 @@ public:
             // mm:569: a prefill of 2-4 tokens (MTP verification) takes gate_up_geglu, the
             // small-batch kernel, in FP32 accumulation whatever the layer's mode
             gate_up_geglu(e, gate, up, static_cast<const uint16_t *>(in), static_cast<uint16_t *>(mid), batch);
+        } else if (batch == 1) {
+            // mm:571-573: gate/up + GeGLU, then down, in one launch where the shapes allow it
+            ffn_block_decode(e, gate, up, down, static_cast<const float *>(in), nullptr, 0.f,
+                             static_cast<float *>(mid), out);
+            return;
         } else {
             // mm:570-571: the fused decode kernel; batches of fp32 tokens take it token by token
             const uint32_t c = cols(gate), r = rows(gate);
@@ -168,6 +173,19 @@ public:
                                      static_cast<float *>(mid) + size_t(t) * r);
         }
         ffn_down(e, down, mid, out, batch, prefill, fast_swa);
+    }
+
+    // The decode block (mm:563 rms when norm_w is given, mm:571-573) in one launch:
+    // mid = GeGLU(gate.n, up.n), out = down.mid, n = in or its RMSNorm (norm_w, eps).
+    // out may alias in.
+    void ffn_block_decode(hipStream_t e, const Tensor &gate, const Tensor &up, const Tensor &down, const float *in,
+                          const float *norm_w, float eps, float *mid, float *out) const {
+        same_shape(gate, up);
+        if (down.shape.at(0) != gate.shape.at(1) || down.shape.at(1) != gate.shape.at(0) ||
+            w_.layout(down) != w_.layout(gate))
+            throw std::runtime_error("down tensor does not match gate/up: " + down.name);
+        check(ns_ffn_block_decode(ctx_, w_.data(gate), w_.data(up), w_.data(down), int(down.type),
+                                  int(w_.layout(gate)), cols(gate), rows(gate), in, norm_w, eps, mid, out, e));
     }
 
     // qkv (mm:311): Q, K and V projections of fp16 `in` ([batch][cols]) into fp32 q, k, v;

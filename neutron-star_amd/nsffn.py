@@ -76,6 +76,7 @@ def lib():
             "ns_rmsnorm_add": [vp, vp, vp, vp, vp, u32, u32, ctypes.c_float, vp, vp],
             "ns_rmsnorm_add_then": [vp, vp, vp, vp, vp, vp, u32, u32, ctypes.c_float, vp, vp, i32, vp],
             "ns_rms_gate_up_geglu_decode": [vp, vp, vp, i32, u32, u32, vp, vp, ctypes.c_float, vp, vp],
+            "ns_ffn_block_decode": [vp, vp, vp, vp, i32, i32, u32, u32, vp, vp, ctypes.c_float, vp, vp, vp],
             "ns_retile": [vp, vp, i32, u32, u32, i32, i32],
             "ns_retile_device": [vp, vp, i32, u32, u32, i32, i32, vp],
             "ns_synth_blocks": [i32, u64, u64, u64, vp, i32],
@@ -346,7 +347,7 @@ class Context:
     def set_tuning(self, key, value):
         """Test hook: override one kernel-selection choice of this context
         (ns_ctx_set_tuning; keys gemv_pf, gemv_waves, gemv_whole, gemv_qslab,
-        gemm_kparts, gemm_q4_reg, mt_mfma, mt_parts, mt_slabs, mt_spw)."""
+        gemm_kparts, gemm_q4_reg, mt_mfma, mt_parts, mt_slabs, mt_spw, block_fused, block_spin)."""
         check(lib().ns_ctx_set_tuning(self.handle, key.encode(), int(value)))
 
     def workspace_bytes(self):
@@ -391,10 +392,13 @@ class Context:
             self.gate_up_geglu_rm32(gate, up, layout, cols, ffn, batch, inp, mid, fast, stream)
         elif prefill:  # mm:569: 2-4 tokens take gate_up_geglu (small-batch kernel, FP32)
             self.gate_up_geglu(gate, up, layout, cols, ffn, batch, inp, mid, stream)
+        elif batch == 1:  # mm:571-573 in one launch (or the same two launches)
+            self.ffn_block_decode(gate, up, down, down_type, layout, cols, ffn, inp, mid, out, stream=stream)
+            return
         else:
             for t in range(batch):
-                self.gate_up_geglu_decode(gate, up, layout, cols, ffn, inp[t * cols:(t + 1) * cols] if batch > 1
-                                          else inp, mid[t * ffn:(t + 1) * ffn] if batch > 1 else mid, stream)
+                self.gate_up_geglu_decode(gate, up, layout, cols, ffn, inp[t * cols:(t + 1) * cols],
+                                          mid[t * ffn:(t + 1) * ffn], stream)
         self.ffn_down(down, down_type, layout, ffn, cols, batch, mid, out, prefill, fast, stream)
 
     def rmsnorm(self, x, weight, rows, width, eps, y, half_out=False, stream=None):
@@ -418,6 +422,14 @@ class Context:
         """rms (mm:563) then gate_up_geglu_decode (mm:571), one launch."""
         check(lib().ns_rms_gate_up_geglu_decode(self.handle, _ptr(wg), _ptr(wu), layout, cols, rows, _ptr(x),
                                                 _ptr(norm_weight), eps, _ptr(h), _stream(stream)))
+
+    def ffn_block_decode(self, wg, wu, wd, down_type, layout, cols, ffn, x, h, y, norm_weight=None, eps=1e-6,
+                         stream=None):
+        """The decode FFN block (mm:571-573) in one launch where the shapes allow it:
+        h = GeGLU(Wg.n, Wu.n), y = Wd.h, n = x or its RMSNorm with norm_weight."""
+        check(lib().ns_ffn_block_decode(self.handle, _ptr(wg), _ptr(wu), _ptr(wd), down_type, layout, cols, ffn,
+                                        _ptr(x), None if norm_weight is None else _ptr(norm_weight), eps, _ptr(h),
+                                        _ptr(y), _stream(stream)))
 
     def embedding(self, w, qtype, layout, cols, rows, ids, batch, scale, out, stream=None):
         """gemma_q6k_embedding (metal:503): out[t] = scale * W[ids[t]]."""

@@ -6,8 +6,8 @@ rescaled to unit RMS as config 4 asks, and the signs keep the synthetic chain fr
 collapsing onto the common component that the uncentred Q4_K weights add to every output.
 
   * the decode stack over 48 distinct seeded full-size layers (config 2's block, the norm
-    fused into the gate/up GEMV), every layer's h and y checked against the oracle fed the
-    same input;
+    fused into the gate/up GEMV; as two launches and as one), every layer's h and y checked
+    against the oracle fed the same input;
   * config 4's per-layer accumulation-mode rule (fast_swa_ffn = prefill && swa &&
     !exact_ffn, metal_engine.mm:565) on a small prefill stack with the Q4_K_M down mix,
     every layer checked against the oracle in its own mode;
@@ -45,11 +45,12 @@ def cdna4(host, qtype, rows, cols):
     return torch.from_numpy(N.retile(host, qtype, cols, rows, N.ROW_MAJOR, N.CDNA4)).cuda()
 
 
-def test_decode_stack_48_distinct_layers(ctx):
+@pytest.mark.parametrize("one_launch", [False, True], ids=["two_launches", "one_launch"])
+def test_decode_stack_48_distinct_layers(ctx, one_launch):
     """Config 2's block at full size over 48 distinct seeded layers, FP32: each layer takes
-    rms(x) fused into the gate/up GEMV, then the Q6_K down projection; h and y are checked
-    against the oracle (O.rmsnorm, then gate/up, then down) fed the GPU's own input, and the
-    next layer takes this layer's y."""
+    rms(x) fused into the gate/up GEMV, then the Q6_K down projection (as two launches, or as
+    the one-launch block); h and y are checked against the oracle (O.rmsnorm, then gate/up,
+    then down) fed the GPU's own input, and the next layer takes this layer's y."""
     D, F = 3840, 15360
     x = torch.from_numpy(N.synth_normal_f32(0x21, D)).cuda()
     h = torch.empty(F, dtype=torch.float32, device="cuda")
@@ -61,8 +62,12 @@ def test_decode_stack_48_distinct_layers(ctx):
         wg, wu, wd = cdna4(hg, N.Q4_K, F, D), cdna4(hu, N.Q4_K, F, D), cdna4(hd, N.Q6_K, D, F)
         nw = signs(s + 5, D)
         y = torch.empty(D, dtype=torch.float32, device="cuda")
-        ctx.rms_gate_up_geglu_decode(wg, wu, N.CDNA4, D, F, x, torch.from_numpy(nw).cuda(), EPS, h)
-        ctx.ffn_down(wd, N.Q6_K, N.CDNA4, F, D, 1, h, y, False, False)
+        if one_launch:
+            ctx.ffn_block_decode(wg, wu, wd, N.Q6_K, N.CDNA4, D, F, x, h, y, norm_weight=torch.from_numpy(nw).cuda(),
+                                 eps=EPS)
+        else:
+            ctx.rms_gate_up_geglu_decode(wg, wu, N.CDNA4, D, F, x, torch.from_numpy(nw).cuda(), EPS, h)
+            ctx.ffn_down(wd, N.Q6_K, N.CDNA4, F, D, 1, h, y, False, False)
         torch.cuda.synchronize()
         xh, hh, yh = x.cpu().numpy(), h.cpu().numpy(), y.cpu().numpy()
         assert np.isfinite(yh).all() and np.any(hh != 0), layer
@@ -71,7 +76,7 @@ def test_decode_stack_48_distinct_layers(ctx):
         assert e1 <= TOL32 and e2 <= TOL32, (layer, e1, e2)
         worst = max(worst, e1, e2)
         x = y
-    print(f"decode stack, 48 layers: worst rel_err {worst:.2e}")
+    print(f"decode stack, 48 layers ({'one launch' if one_launch else 'two launches'}): worst rel_err {worst:.2e}")
 
 
 def test_stack_prefill_mode_rule(ctx):
@@ -118,8 +123,8 @@ def test_stack_prefill_mode_rule(ctx):
 
 @pytest.mark.parametrize("nlayers", [6, 48])
 def test_decode_step_graph_replay_matches_eager(ctx, nlayers):
-    """A decode step of the stack (config 4: Q4_K_M down mix, rms fused into every
-    gate/up, the final rms and the full 262,144-row lm-head at the end) captured once into a
+    """A decode step of the stack (config 4: Q4_K_M down mix, each layer's rms, gate/up and
+    down in one launch, the final rms and the full 262,144-row lm-head at the end) captured once into a
     HIP graph and replayed three times, with eager work and synchronisations between
     replays; every replay's logits must equal the eager step's bit for bit.  Between the
     capture and the replays the same context runs a batch-1024 prefill block in both modes,
@@ -145,8 +150,7 @@ def test_decode_step_graph_replay_matches_eager(ctx, nlayers):
     def step():
         inp = xd
         for g, u, d, dt, nw in layers:
-            ctx.rms_gate_up_geglu_decode(g, u, N.CDNA4, D, F, inp, nw, EPS, h)
-            ctx.ffn_down(d, dt, N.CDNA4, F, D, 1, h, y, False, False)
+            ctx.ffn_block_decode(g, u, d, dt, N.CDNA4, D, F, inp, h, y, norm_weight=nw, eps=EPS)
             inp = y
         ctx.rmsnorm(y, out_norm, 1, D, EPS, xs)
         ctx.matmul(lm, N.Q6_K, N.CDNA4, D, V, 1, xs, logits)
