@@ -1239,8 +1239,9 @@ uint32_t mt_tokens(uint32_t batch, bool xh) { return xh && batch <= 2 ? 2u : 4u;
 // bounded: a workgroup whose spin limit runs out records it in status and goes on, so every
 // wave exits, and the slabs finished after that are written as NaN (the limit is seconds
 // long).  The last slab to finish clears the counters for the next launch.  Per row and part
-// the arithmetic and its order are those of the two launches (gemv_kernel's whole-slab
-// gate/up and its k-workgroups-per-slab down), so the results are the same bit for bit.
+// the arithmetic and its order are those of gemv_kernel's whole-slab gate/up and its
+// k-workgroups-per-slab down, the plans the two launches take at the model's shape (3840 x
+// 15360), so there the results are the same bit for bit.
 constexpr uint32_t kBlockMaxW = 16;
 constexpr uint32_t kCtrStride = 32;  // one counter per 128-byte line
 
