@@ -66,6 +66,30 @@ __device__ __forceinline__ uint32_t bload2(rsrc_t r, uint32_t voff, uint32_t sof
     return __builtin_amdgcn_raw_buffer_load_b16(r, int(voff), int(soff), 0);
 }
 
+// Lane exchanges inside a row of 16 lanes by DPP (no LDS round trip): dpp_ctrl 0xB1 and 0x4E
+// are quad_perm [1,0,3,2] and [2,3,0,1] (lane ^ 1, lane ^ 2), 0x141 row_half_mirror (lane i of
+// an 8-lane half takes lane 7 - i), 0x140 row_mirror (lane i of the row takes lane 15 - i).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// Sum over 8 consecutive lanes, in every lane of them: a + a^1, then + (^2), then the other
+// quad's sum (the values a butterfly with lane ^ 4 would add, in the same order).
+__device__ __forceinline__ float sum8(float s) {
+    s += dpp<0xB1>(s);
+    s += dpp<0x4E>(s);
+    return s + dpp<0x141>(s);
+}
+// Largest value of the wave (every lane's value >= 0), wave-uniform.
+__device__ __forceinline__ float wave_max(float m) {
+    m = __builtin_fmaxf(m, dpp<0xB1>(m));
+    m = __builtin_fmaxf(m, dpp<0x4E>(m));
+    m = __builtin_fmaxf(m, dpp<0x141>(m));
+    m = __builtin_fmaxf(m, dpp<0x140>(m));
+    const auto rl = [&](int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m), l)); };
+    return __builtin_fmaxf(__builtin_fmaxf(rl(0), rl(16)), __builtin_fmaxf(rl(32), rl(48)));
+}
+
 // Four bytes (values < 1024) -> four exact fp16 values byte - bias, in element order.
 // (0x6400 | b) is the fp16 1024 + b; one packed add removes 1024 + bias.
 __device__ __forceinline__ void bytes_to_f16(uint32_t v, half2_t bias, uint32_t &lo, uint32_t &hi) {
@@ -183,17 +207,16 @@ __global__ __launch_bounds__(kMaxWaves * 64) void gemv_mfma_kernel(
     //    fp16 hi part cannot overflow, and tiny tokens keep their bits out of fp16's subnormals;
     //  - the Q4_K group sums enter as xs * 2^-(e+5) (|xs| <= 32 * max|x|), for fp16 tokens too.
     // Both are exact; the results are scaled back by the inverse powers.
-    float ascale[NT], oscale[NT], xsscale[NT], minfac[NT];
+    float oscale[NT], minfac[NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) ascale[t] = oscale[t] = xsscale[t] = minfac[t] = 1.f;
+    for (int t = 0; t < NT; ++t) oscale[t] = minfac[t] = 1.f;
+    // e + 128 of every token, one byte each: a lane picks its token's with one bit-field
+    // extract (selecting from a register array by a lane-varying index would put the array in
+    // scratch, and the scratch load's wait would also wait for the weights in flight)
+    uint32_t epack = 128u * 0x01010101u;
+    auto p2 = [](int k) { return __builtin_bit_cast(float, uint32_t(127 + k) << 23); };
+    auto e_of = [&](uint32_t t) { return int(__builtin_amdgcn_ubfe(epack, 8 * (t & 3), 8)) - 128; };
     const uint32_t nq = nk / 4;  // 4-column quads per token
-    auto pick = [](const float (&a)[NT], uint32_t t) {
-        float v = a[0];
-#pragma unroll
-        for (int u = 1; u < NT; ++u)
-            if (uint32_t(u) == t) v = a[u];
-        return v;
-    };
     // One round of loads: quad i = r * blockDim + tid (token i / nq) for r < kStage; the plan
     // gives every workgroup enough threads (64 * waves * kStage >= NT * nq).  All loads are in
     // flight before the first use.
@@ -238,24 +261,24 @@ __global__ __launch_bounds__(kMaxWaves * 64) void gemv_mfma_kernel(
         }
 #pragma unroll
         for (int u = 0; u < NT; ++u) {
-#pragma unroll
-            for (int s = 32; s >= 1; s >>= 1) mx[u] = __builtin_fmaxf(mx[u], __shfl_xor(mx[u], s));
+            mx[u] = wave_max(mx[u]);
             if (lane == 0) wmax[wave][u] = mx[u];
         }
-        __syncthreads();
-        auto p2 = [](int k) { return __builtin_bit_cast(float, uint32_t(127 + k) << 23); };
+        // a bare barrier: __syncthreads() would also wait for the first super-block's weights
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_barrier();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        epack = 0;
 #pragma unroll
         for (int u = 0; u < NT; ++u) {
             float m = 0.f;
             for (uint32_t v = 0; v < nw; ++v) m = __builtin_fmaxf(m, wmax[v][u]);
             const int E = int((__builtin_bit_cast(uint32_t, m) >> 23) & 0xFF) - 127;  // floor(log2 m), normal m
             const int e = m >= 1.17549435e-38f && E < 128 ? __builtin_elementwise_max(E - 14, -100) : 0;
-            if constexpr (!XH) {
-                ascale[u] = p2(-e);
-                oscale[u] = p2(e);
-            }
-            xsscale[u] = p2(-(e + 5));
+            if constexpr (!XH) oscale[u] = p2(e);
             minfac[u] = XH ? p2(e + 5) : 32.f;
+            epack |= uint32_t(e + 128) << (8 * u);
         }
     }
 #pragma unroll
@@ -271,7 +294,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void gemv_mfma_kernel(
             hi01 = __builtin_bit_cast(uint32_t, half2_t{_Float16(v.x), _Float16(v.y)});
             hi23 = __builtin_bit_cast(uint32_t, half2_t{_Float16(v.z), _Float16(v.w)});
         } else {
-            const float4_t v = xv[r] * pick(ascale, t);
+            const float4_t v = xv[r] * p2(-e_of(t));
             const half2_t h01{_Float16(v.x), _Float16(v.y)}, h23{_Float16(v.z), _Float16(v.w)};
             const half2_t l01{_Float16(v.x - float(h01.x)), _Float16(v.y - float(h01.y))};
             const half2_t l23{_Float16(v.z - float(h23.x)), _Float16(v.w - float(h23.y))};
@@ -286,10 +309,8 @@ __global__ __launch_bounds__(kMaxWaves * 64) void gemv_mfma_kernel(
             // group sum of 32 columns = 8 quads held by 8 consecutive lanes (nq and blockDim are
             // multiples of 8): a fixed butterfly, times 2^-(e+5), split into fp16 hi + lo
             float s = (xv[r].x + xv[r].y) + (xv[r].z + xv[r].w);
-            s += __shfl_xor(s, 1);
-            s += __shfl_xor(s, 2);
-            s += __shfl_xor(s, 4);
-            s *= pick(xsscale, t);
+            s = sum8(s);
+            s *= p2(-(e_of(t) + 5));
             if ((q & 7) == 0 && t < NT) {
                 const uint32_t gi = q >> 3;
                 const _Float16 h = _Float16(s);
@@ -425,25 +446,25 @@ __global__ __launch_bounds__(kMaxWaves * 64) void gemv_mfma_kernel(
     };
 
     // ---- main loop: compute one super-block while the next one's weights load ---------------
-    // Two buffers alternate.  The end test comes before each prefetch, so every prefetch is
-    // consumed on every path: a load that a path leaves unused is sunk by the compiler past the
-    // compute into the path that uses it, which serialises load and compute.  The scheduling
-    // barrier keeps the prefetch ahead of the compute.
-    // Every wave runs it (one past the last slab on the clamped last slab, its results
-    // dropped), and every wave has at least one super-block (the plan keeps P <= nsb): a branch
-    // around the loop would leave the prologue's loads unused on one path, and the compiler
-    // would sink them under it.
+    // Two buffers alternate.  The first iteration is peeled: its prefetch is unconditional
+    // (clamped into the tensor; a wave with one super-block drops it) and pinned by a signal
+    // fence, so it leaves right after the staging barrier.  Entering the loop with the
+    // prologue's buffer instead made the compiler copy that buffer into the loop's registers,
+    // which waited for its loads before the first prefetch could issue.  Inside the loop the end
+    // test comes before each prefetch, so every prefetch is consumed on every path: a load that a
+    // path leaves unused is sunk by the compiler past the compute into the path that uses it,
+    // which serialises load and compute.  The scheduling barrier keeps the prefetch ahead of the
+    // compute.  Every wave runs it (one past the last slab on the clamped last slab, its results
+    // dropped), and every wave has at least one super-block (the plan keeps P <= nsb).
     {
         uint32_t sb = wsb0;
-        while (true) {
-            if (sb + 1 == wsb1) {
-                compute(ra, sb);
-                break;
-            }
-            load(sb + 1, rb);
-            __builtin_amdgcn_sched_barrier(0);
-            compute(ra, sb);
-            ++sb;
+        const bool more = sb + 1 != wsb1;
+        load(__builtin_elementwise_min(sb + 1, nb - 1), rb);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(ra, sb);
+        ++sb;
+        while (more) {
             if (sb + 1 == wsb1) {
                 compute(rb, sb);
                 break;
@@ -451,6 +472,14 @@ __global__ __launch_bounds__(kMaxWaves * 64) void gemv_mfma_kernel(
             load(sb + 1, ra);
             __builtin_amdgcn_sched_barrier(0);
             compute(rb, sb);
+            ++sb;
+            if (sb + 1 == wsb1) {
+                compute(ra, sb);
+                break;
+            }
+            load(sb + 1, rb);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(ra, sb);
             ++sb;
         }
     }
