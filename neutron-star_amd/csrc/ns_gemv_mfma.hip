@@ -156,6 +156,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void gemv_mfma_kernel(
     __shared__ __attribute__((aligned(16))) _Float16 xl[(kZero + 1) * kStripe];
     __shared__ __attribute__((aligned(16))) _Float16 xsl[kMaxSb][2][NT][8];  // Q4_K group sums (hi, lo)
     __shared__ float wmax[kMaxWaves][NT];
+    __shared__ float xsc[kMaxSb][NT];  // Q4_K, fp16 x: 2^(e+5) of each super-block's group sums
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, nw = blockDim.x >> 6;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -205,7 +206,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void gemv_mfma_kernel(
     // Per-token powers of two, from the largest |x| of the workgroup's columns (2^E <= max < 2^(E+1)):
     //  - fp32 tokens enter the MFMA as x * 2^-e, e = E - 14, so the largest is in [2^14, 2^15): the
     //    fp16 hi part cannot overflow, and tiny tokens keep their bits out of fp16's subnormals;
-    //  - the Q4_K group sums enter as xs * 2^-(e+5) (|xs| <= 32 * max|x|), for fp16 tokens too.
+    //  - the Q4_K group sums enter as xs * 2^-(e+5) (|xs| <= 32 * max|x|); for fp16 tokens e comes
+    //    from the super-block's own largest |x| (the min term of each super-block is scaled
+    //    back on its own).
     // Both are exact; the results are scaled back by the inverse powers.
     float oscale[NT], minfac[NT];
 #pragma unroll
@@ -247,7 +250,10 @@ __global__ __launch_bounds__(kMaxWaves * 64) void gemv_mfma_kernel(
             xv[r] = t < batch ? v : float4_t{0.f, 0.f, 0.f, 0.f};
         }
     }
-    if constexpr (!XH || !Q6) {
+    // fp32 tokens: one power of two per token for the workgroup's columns (the A rows carry it
+    // into every super-block).  fp16 tokens only scale the Q4_K group sums, per super-block, in
+    // the store loop below: no workgroup-wide maximum, no barrier.
+    if constexpr (!XH) {
         float mx[NT] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int r = 0; r < kStage; ++r) {
@@ -276,8 +282,8 @@ __global__ __launch_bounds__(kMaxWaves * 64) void gemv_mfma_kernel(
             for (uint32_t v = 0; v < nw; ++v) m = __builtin_fmaxf(m, wmax[v][u]);
             const int E = int((__builtin_bit_cast(uint32_t, m) >> 23) & 0xFF) - 127;  // floor(log2 m), normal m
             const int e = m >= 1.17549435e-38f && E < 128 ? __builtin_elementwise_max(E - 14, -100) : 0;
-            if constexpr (!XH) oscale[u] = p2(e);
-            minfac[u] = XH ? p2(e + 5) : 32.f;
+            oscale[u] = p2(e);
+            minfac[u] = 32.f;
             epack |= uint32_t(e + 128) << (8 * u);
         }
     }
@@ -310,7 +316,18 @@ __global__ __launch_bounds__(kMaxWaves * 64) void gemv_mfma_kernel(
             // multiples of 8): a fixed butterfly, times 2^-(e+5), split into fp16 hi + lo
             float s = (xv[r].x + xv[r].y) + (xv[r].z + xv[r].w);
             s = sum8(s);
-            s *= p2(-(e_of(t) + 5));
+            int eg = e_of(t);
+            if constexpr (XH) {
+                // the wave's 64 quads are one super-block of one token (nq is a multiple of 64):
+                // its largest |x| sets the group sums' power of two
+                const float4_t v = xv[r];
+                const float m = wave_max(__builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
+                                                         __builtin_fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w))));
+                const int E = int((__builtin_bit_cast(uint32_t, m) >> 23) & 0xFF) - 127;
+                eg = m >= 1.17549435e-38f && E < 128 ? __builtin_elementwise_max(E - 14, -100) : 0;
+                if (lane == 0 && t < NT) xsc[q >> 6][t] = p2(eg + 5);
+            }
+            s *= p2(-(eg + 5));
             if ((q & 7) == 0 && t < NT) {
                 const uint32_t gi = q >> 3;
                 const _Float16 h = _Float16(s);
@@ -427,6 +444,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void gemv_mfma_kernel(
                     S[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, __builtin_bit_cast(half8_t, bhi[t]), S[t], 0, 0, 0);
             }
             const uint32_t si = sb - sb_lo;
+            float mf[NT];
+#pragma unroll
+            for (int v = 0; v < NT; ++v) mf[v] = XH ? xsc[si][v] : minfac[v];
             u32x2 am = *reinterpret_cast<const u32x2 *>(&xsl[si][o >> 1][n & 3][4 * (o & 1)]);
             if (!xs_valid) am = u32x2{0u, 0u};
 #pragma unroll
@@ -440,7 +460,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void gemv_mfma_kernel(
                 const float d = lo_half(r.hdr[t].x), dmin = hi_half(r.hdr[t].x);
 #pragma unroll
                 for (int v = 0; v < 4; ++v)
-                    acc[t][v] = __builtin_fmaf(d, S[t][v], __builtin_fmaf(-dmin * minfac[v], mn[v], acc[t][v]));
+                    acc[t][v] = __builtin_fmaf(d, S[t][v], __builtin_fmaf(-dmin * mf[v], mn[v], acc[t][v]));
             }
         }
     };
