@@ -637,10 +637,10 @@ auto dispatch_mfma(int type, bool pair, bool xh, Fn &&fn) {
 
 }  // namespace
 
-// The gate/up pair at one or two tokens stays on the VALU kernel: its two-token instance
-// measured 26.5 us against 28-33 us here (MI355X); every other shape is faster here.
+// The gate/up pair (fp16 x) from two tokens on: at two tokens 22.7-22.9 us here against
+// 25.1-25.2 us for the VALU kernel (same-box A/B, MI355X); every other shape is faster here too.
 bool gemv_mfma_eligible(int layout, bool pair, bool xh, uint32_t batch, const Tuning &t) {
-    return layout == CDNA4 && t.mt_mfma != 0 && (!pair || (xh && batch > 2));
+    return layout == CDNA4 && t.mt_mfma != 0 && (!pair || (xh && batch >= 2));
 }
 
 void gemv_mfma_workspace_need(uint32_t cols, uint32_t rows, bool pair, const Tuning &t, size_t *partial_floats,
