@@ -93,7 +93,9 @@ int ns_ctx_workspace_bytes(const ns_ctx *ctx, uint64_t *bytes);
  * "mt_slabs" / "mt_spw" (> 0: that MFMA kernel's column parts per workgroup,
  * slabs per workgroup, super-blocks per wave), "block_fused" (0: the decode
  * FFN block as two launches), "block_spin" (> 0: the one-launch block's bound on
- * a wait, in polls; tests shorten it to exercise the bound).  Results stay within
+ * a wait, in polls; tests shorten it to exercise the bound), "gemm_rs" (0: split-K
+ * FP16-mode prefill GEMMs finish by the last part to arrive instead of the
+ * reduce-scatter; > 1: the reduce-scatter's bound on its wait).  Results stay within
  * the same tolerances; engines leave the defaults. */
 int ns_ctx_set_tuning(ns_ctx *ctx, const char *key, int value);
 

@@ -210,6 +210,7 @@ extern "C" int ns_ctx_set_tuning(ns_ctx *ctx, const char *key, int value) {
     else if (k == "mt_spw") t.mt_spw = value;
     else if (k == "block_fused") t.block_fused = value;
     else if (k == "block_spin") t.block_spin = value;
+    else if (k == "gemm_rs") t.gemm_rs = value;
     else return fail(NS_ERR_ARG, "ns_ctx_set_tuning: unknown key " + k);
     return NS_OK;
 }

@@ -99,7 +99,8 @@ template <int TYPE, bool PAIR>
 __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
     const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, const uint16_t *__restrict__ x,
     void *__restrict__ out, float *__restrict__ partial, uint32_t *__restrict__ counters, uint32_t cols,
-    uint32_t rows, uint32_t batch, uint32_t ntok_tiles, uint32_t ncol_tiles, uint32_t kparts, uint32_t wbytes) {
+    uint32_t rows, uint32_t batch, uint32_t ntok_tiles, uint32_t ncol_tiles, uint32_t kparts, uint32_t wbytes,
+    uint32_t rs_spin) {
     constexpr bool Q4 = TYPE == Q4_K;
     using Raw = typename std::conditional<Q4, RawQ4, RawQ6>::type;
     // Four separate LDS objects rather than one array: the compiler then sees that a DMA into
@@ -108,7 +109,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
     __shared__ __attribute__((aligned(16))) u32x4 Xs0[TT * 8], Xs1[TT * 8], Xs2[TT * 8], Xs3[TT * 8];
     static_assert(XBUF == 4, "one LDS object per x buffer");
     auto xbuf = [&](int buf) -> u32x4 * { return buf == 0 ? Xs0 : buf == 1 ? Xs1 : buf == 2 ? Xs2 : Xs3; };
-    __shared__ uint32_t last_flag;
+    __shared__ uint32_t last_flag, late_flag;
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, hl = lane >> 5;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -477,6 +478,93 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
         return (uint32_t(i) * 32 + 8 * uint32_t(v >> 2) + uint32_t(v & 3)) * rstride + lane_off[j];
     };
     auto pbase = [&](uint32_t part) -> char * { return reinterpret_cast<char *>(partial + part * pstride); };
+    if (rs_spin != 0) {
+        // Reduce-scatter (the host launches it only when the whole grid fits on the device at
+        // once, so the kparts workgroups of a tile run together): part kp owns token sub-tiles
+        // [own_lo, own_hi) of the tile.  Each part stores the sub-tiles it does not own, keeps
+        // its own in LDS (slot k in x buffer k, free after the main loop), counts one arrival on
+        // written[tile] once its stores are acknowledged, waits until every part has, then adds
+        // the parts of its own sub-tiles in part order (its own from LDS) and writes them.  Every
+        // part reads and writes a 1/kparts share, where the last arrival of the other form reads
+        // every part alone.  The wait is bounded: a part whose limit runs out writes its
+        // sub-tiles as NaN.  The last part past the wait clears both counters.
+        const uint32_t ntiles = ntok_tiles * ncol_tiles;
+        uint32_t *written = counters + tile, *departed = counters + ntiles + tile;
+        const uint32_t own_lo = kp * MI / kparts, own_hi = (kp + 1) * MI / kparts;
+        __syncthreads();  // every wave is past its last read of the x buffers
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+            if (uint32_t(i) >= own_lo && uint32_t(i) < own_hi) {
+                float *slot = reinterpret_cast<float *>(xbuf(int(uint32_t(i) - own_lo) & 3));
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) slot[(v * NJ + j) * kThreads + tid] = acc[i][j][v];
+            } else {
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j)
+                        __hip_atomic_store(reinterpret_cast<float *>(pbase(kp) + poff(i, v, j)), acc[i][j][v],
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __syncthreads();
+        if (tid == 0) {
+            __hip_atomic_fetch_add(written, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            uint32_t late = 0;
+            for (uint32_t it = 0; __hip_atomic_load(written, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < kparts;) {
+                __builtin_amdgcn_s_sleep(2);
+                if (++it >= rs_spin) {
+                    late = 1;
+                    break;
+                }
+            }
+            late_flag = late;
+            if (__hip_atomic_fetch_add(departed, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == kparts - 1) {
+                __hip_atomic_store(written, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(departed, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        __syncthreads();
+        const bool late = late_flag != 0;
+        for (uint32_t i = own_lo; i < own_hi; ++i) {
+            const float *slot = reinterpret_cast<const float *>(xbuf(int(i - own_lo) & 3));
+            float sum[16][NJ];
+            for (uint32_t p0 = 0; p0 < kparts; p0 += 4) {
+                float pv[4][16][NJ];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    // this part's own slot holds no value for these sub-tiles: read from LDS below
+                    const uint32_t part = __builtin_elementwise_min(p0 + uint32_t(u), kparts - 1);
+#pragma unroll
+                    for (int v = 0; v < 16; ++v)
+#pragma unroll
+                        for (int j = 0; j < NJ; ++j)
+                            pv[u][v][j] = __hip_atomic_load(reinterpret_cast<float *>(pbase(part) + poff(int(i), v, j)),
+                                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) {
+                        float t = p0 == 0 ? 0.f : sum[v][j];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            const uint32_t part = p0 + uint32_t(u);
+                            const float val = part == kp ? slot[(v * NJ + j) * kThreads + tid] : pv[u][v][j];
+                            t = part == 0 ? val : part < kparts ? t + val : t;
+                        }
+                        sum[v][j] = t;
+                    }
+            }
+            write_out(int(i), [&](int v, int j) { return late ? __builtin_nanf("") : sum[v][j]; });
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -532,6 +620,25 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
     }
 }
 
+// Workgroups of one instance the device holds at once (one per CU at 128 KiB of LDS), per device.
+template <class K>
+uint64_t resident_wgs(K kernel) {
+    static int cache[64][3] = {};
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    const int slot = kernel == &gemm_f16_kernel<Q4_K, true> ? 0 : kernel == &gemm_f16_kernel<Q4_K, false> ? 1 : 2;
+    int &n = cache[dev & 63][slot];
+    if (n == 0) {
+        int wgs = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&wgs, kernel, kThreads, 0) != hipSuccess || wgs <= 0 ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            n = -1;  // unknown: never taken as room
+        else
+            n = wgs * cus;
+    }
+    return n > 0 ? uint64_t(n) : 0;
+}
+
 struct F16Plan {
     uint32_t ntok, ncol, kparts;
 };
@@ -556,7 +663,7 @@ void gemm_f16_workspace_need(uint32_t cols, uint32_t rows, uint32_t batch, bool 
                              size_t *part_floats, size_t *counters) {
     const F16Plan p = plan_f16(cols, rows, batch, pair, t);
     *part_floats = p.kparts > 1 ? size_t(p.kparts) * (pair ? 2 : 1) * (p.ntok * TT) * (p.ncol * (pair ? TC / 2 : TC)) : 0;
-    *counters = size_t(p.ntok) * p.ncol;
+    *counters = 2 * size_t(p.ntok) * p.ncol;  // arrivals; and departures of the reduce-scatter
 }
 
 hipError_t launch_gemm_f16(int type, const uint8_t *w, const uint8_t *up, const uint16_t *x, void *out, uint32_t cols,
@@ -566,15 +673,14 @@ hipError_t launch_gemm_f16(int type, const uint8_t *w, const uint8_t *up, const 
     const F16Plan p = plan_f16(cols, rows, batch, pair, t);
     const dim3 grid(p.ntok * p.ncol * p.kparts), block(kThreads);
     const uint32_t wbytes = rows * (cols / kQK) * block_bytes(type);
-    if (pair)
-        gemm_f16_kernel<Q4_K, true><<<grid, block, 0, stream>>>(w, up, x, out, partial, counters, cols, rows, batch,
-                                                                p.ntok, p.ncol, p.kparts, wbytes);
-    else if (type == Q4_K)
-        gemm_f16_kernel<Q4_K, false><<<grid, block, 0, stream>>>(w, w, x, out, partial, counters, cols, rows, batch,
-                                                                 p.ntok, p.ncol, p.kparts, wbytes);
-    else
-        gemm_f16_kernel<Q6_K, false><<<grid, block, 0, stream>>>(w, w, x, out, partial, counters, cols, rows, batch,
-                                                                 p.ntok, p.ncol, p.kparts, wbytes);
+    // the reduce-scatter needs every part of a tile running at once: the whole grid resident
+    const auto kernel = pair ? &gemm_f16_kernel<Q4_K, true>
+                             : type == Q4_K ? &gemm_f16_kernel<Q4_K, false> : &gemm_f16_kernel<Q6_K, false>;
+    uint32_t rs_spin = 0;
+    if (p.kparts > 1 && MI % p.kparts == 0 && t.gemm_rs != 0 && uint64_t(grid.x) <= resident_wgs(kernel))
+        rs_spin = t.gemm_rs > 1 ? uint32_t(t.gemm_rs) : 1u << 22;  // 2^22 polls of s_sleep 2: seconds
+    kernel<<<grid, block, 0, stream>>>(w, pair ? up : w, x, out, partial, counters, cols, rows, batch, p.ntok, p.ncol,
+                                       p.kparts, wbytes, rs_spin);
     return hipGetLastError();
 }
 

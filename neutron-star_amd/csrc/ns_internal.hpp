@@ -28,6 +28,7 @@ struct Tuning {
     int mt_spw = 0;       // > 0: its super-blocks per wave (more workgroups per slab)
     int block_fused = 1;  // 0: the decode FFN block as two launches instead of one
     int block_spin = 0;   // > 0: that launch's bound on a down workgroup's wait (polls)
+    int gemm_rs = 1;      // 0: split-K FP16-mode GEMMs finish by the last arrival; > 1: reduce-scatter wait bound
 };
 
 // Workspace owned by ns_ctx: fp32 partial sums and per-slab arrival counters

@@ -347,7 +347,7 @@ class Context:
     def set_tuning(self, key, value):
         """Test hook: override one kernel-selection choice of this context
         (ns_ctx_set_tuning; keys gemv_pf, gemv_waves, gemv_whole, gemv_qslab,
-        gemm_kparts, gemm_q4_reg, mt_mfma, mt_parts, mt_slabs, mt_spw, block_fused, block_spin)."""
+        gemm_kparts, gemm_q4_reg, mt_mfma, mt_parts, mt_slabs, mt_spw, block_fused, block_spin, gemm_rs)."""
         check(lib().ns_ctx_set_tuning(self.handle, key.encode(), int(value)))
 
     def workspace_bytes(self):

@@ -129,3 +129,61 @@ def test_fp16_gate_up_one_hot(ctx, layout):
     ref = O.gate_up_geglu_prefill(O.ROW_MAJOR, hg, hu, cols, rows, len(ks), f16_bits(x), 1)
     step = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -14))) - 10)
     assert np.all(np.abs(got - ref) <= step)
+
+
+def _down_case(qtype, batch, seed):
+    cols, rows = 15360, 3840
+    host = N.synth_weights(qtype, seed, rows, cols)
+    w = dev(host, qtype, cols, rows, N.CDNA4)
+    xd = torch.from_numpy(N.synth_normal_f16(seed + 1, batch * cols).view(np.int16).reshape(batch, cols)).cuda()
+    return cols, rows, w, xd
+
+
+def _run_down(ctx, qtype, cols, rows, batch, w, xd):
+    y = torch.full((batch, rows), float("nan"), dtype=torch.float32, device="cuda")
+    ctx.ffn_down(w, qtype, N.CDNA4, cols, rows, batch, xd, y, half_input=True, fast_swa=True)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+@pytest.mark.parametrize("kparts", [0, 2, 8], ids=["plan", "split2", "split8"])
+@pytest.mark.parametrize("batch", [1024, 300])
+@pytest.mark.parametrize("qtype", [N.Q4_K, N.Q6_K], ids=["q4k", "q6k"])
+def test_split_k_reduce_scatter_equals_last_arrival(ctx, tune, qtype, batch, kparts):
+    """The FP16-mode down projection (3840 x 15360, CDNA4) finishes its split-K tiles either by
+    a reduce-scatter (every part adds the parts of its own token sub-tiles; the default when the
+    grid fits the device at once) or by the last part to arrive (tuning key gemm_rs 0).  Both add
+    the same fp32 parts in part order, so the outputs are equal bit for bit."""
+    if kparts:
+        tune("gemm_kparts", kparts)
+    cols, rows, w, xd = _down_case(qtype, batch, 0xD0 + batch)
+    a = _run_down(ctx, qtype, cols, rows, batch, w, xd)
+    tune("gemm_rs", 0)
+    b = _run_down(ctx, qtype, cols, rows, batch, w, xd)
+    assert np.isfinite(a).all()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_split_k_reduce_scatter_bounded_wait(ctx, tune):
+    """The reduce-scatter's wait for the other parts is bounded.  Forced down to two polls from
+    the host (every wave still exits normally), a part whose wait ran out writes its token
+    sub-tiles (32 tokens each) as NaN and every other sub-tile is the normal result; the next
+    launch with the default bound is whole again (the last part clears the counters)."""
+    qtype, batch = N.Q6_K, 1024
+    cols, rows, w, xd = _down_case(qtype, batch, 0xE0)
+    want = _run_down(ctx, qtype, cols, rows, batch, w, xd)
+    tune("gemm_rs", 2)
+    got = _run_down(ctx, qtype, cols, rows, batch, w, xd)
+    tune("gemm_rs", 1)
+    again = _run_down(ctx, qtype, cols, rows, batch, w, xd)
+    blocks = got.reshape(batch // 32, 32, rows // 256, 256).transpose(0, 2, 1, 3)
+    ref = want.reshape(batch // 32, 32, rows // 256, 256).transpose(0, 2, 1, 3)
+    nan_blocks = 0
+    for a in range(blocks.shape[0]):
+        for c in range(blocks.shape[1]):
+            if np.isnan(blocks[a, c]).all():
+                nan_blocks += 1
+            else:
+                assert np.array_equal(blocks[a, c].view(np.uint32), ref[a, c].view(np.uint32)), (a, c)
+    print(f"bounded wait: {nan_blocks} of {blocks.shape[0] * blocks.shape[1]} sub-tiles ran out")
+    assert np.array_equal(again.view(np.uint32), want.view(np.uint32))
