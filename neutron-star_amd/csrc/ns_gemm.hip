@@ -293,7 +293,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, const uint16_t *__restrict__ x,
     const uint16_t *__restrict__ xsums, void *__restrict__ out, float *__restrict__ partial,
     uint32_t *__restrict__ counters, uint32_t cols, uint32_t rows, uint32_t batch, uint32_t ntok_tiles,
-    uint32_t ncol_tiles, uint32_t kparts_total, uint32_t wbytes) {
+    uint32_t ncol_tiles, uint32_t kparts_total, uint32_t wbytes, uint32_t rs_spin) {
     constexpr bool Q4 = TYPE == Q4_K;
     constexpr bool F16 = ACC == ACC_FP16;  // fp16 tiles (ns_tile16.hpp) instead of exact ones
     constexpr uint32_t kRawLoads = Q4 ? 2 : (LAYOUT == CDNA4 ? 6 : 41);  // vector loads per load_raw
@@ -303,7 +303,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     __shared__ float colInv[TC];  // FP16 mode: 1/c of each column's row
     // Q4_K min factors per column: 8 fp16 values b_g, then their 8 rounding residues
     __shared__ __attribute__((aligned(16))) _Float16 colB[2][Q4 ? TC * 16 : 16];
-    __shared__ uint32_t last_flag;
+    __shared__ uint32_t last_flag, late_flag;
 
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -599,6 +599,105 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
         return (uint32_t(i) * 32 + 8 * uint32_t(v >> 2) + uint32_t(v & 3)) * rstride + lo[jj];
     };
     auto pbase = [&](uint32_t part) -> char * { return reinterpret_cast<char *>(partial + part * pstride); };  // uniform
+    if (rs_spin != 0) {
+        // Reduce-scatter (launched only when the whole grid fits on the device at once, so the
+        // kparts workgroups of a tile run together; kparts divides MI): part kp owns token
+        // sub-tiles [own_lo, own_hi) of every wave.  Each part stores the sub-tiles it does not
+        // own, parks its own in LDS (slot 0 in the x tiles, slot 1 in the weight tiles, both
+        // free after the main loop), counts one arrival on written[tile] once its stores are
+        // acknowledged, waits until every part has, then adds the parts of its own sub-tiles in
+        // part order (its own from LDS) and writes them.  The wait is bounded: a part whose limit
+        // runs out writes its sub-tiles as NaN.  The last part past the wait clears both counters.
+        const uint32_t ntiles = ntok_tiles * ncol_tiles;
+        uint32_t *written = counters + tile, *departed = counters + ntiles + tile;
+        const uint32_t own_lo = kp * MI / kparts, own_hi = (kp + 1) * MI / kparts;
+        auto slot_of = [&](uint32_t k) -> float * {
+            return k == 0 ? reinterpret_cast<float *>(&Xs[0][0]) : reinterpret_cast<float *>(&Ws[0][0]);
+        };
+        __syncthreads();  // every wave is past its last read of the tiles
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+            if (uint32_t(i) >= own_lo && uint32_t(i) < own_hi) {
+                float *slot = slot_of(uint32_t(i) - own_lo);
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+#pragma unroll
+                    for (int jj = 0; jj < NJ; ++jj) slot[(v * NJ + jj) * kThreads + tid] = acc[i][jj][v];
+            } else {
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+#pragma unroll
+                    for (int jj = 0; jj < NJ; ++jj)
+                        __hip_atomic_store(reinterpret_cast<float *>(pbase(kp) + poff(lane_off, i, v, jj)),
+                                           acc[i][jj][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __syncthreads();
+        if (tid == 0) {
+            __hip_atomic_fetch_add(written, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            uint32_t late = 0;
+            for (uint32_t it = 0; __hip_atomic_load(written, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < kparts;) {
+                __builtin_amdgcn_s_sleep(2);
+                if (++it >= rs_spin) {
+                    late = 1;
+                    break;
+                }
+            }
+            late_flag = late;
+            if (__hip_atomic_fetch_add(departed, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == kparts - 1) {
+                __hip_atomic_store(written, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(departed, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        __syncthreads();
+        const bool late = late_flag != 0;
+        for (uint32_t i = own_lo; i < own_hi; ++i) {
+            const float *slot = slot_of(i - own_lo);
+            float sum[16][NJ];
+            for (uint32_t p0 = 0; p0 < kparts; p0 += 2) {  // two parts per round trip
+                float pv[2][16][NJ];
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    // this part's own slot holds no value for these sub-tiles: read from LDS below
+                    const uint32_t part = __builtin_elementwise_min(p0 + uint32_t(u), kparts - 1);
+                    uint32_t lo[NJ];  // recomputed per round trip, not kept live (see the last arrival)
+#pragma unroll
+                    for (int jj = 0; jj < NJ; ++jj) {
+                        lo[jj] = lane_off[jj];
+                        asm volatile("" : "+v"(lo[jj]));
+                    }
+#pragma unroll
+                    for (int v = 0; v < 16; ++v)
+#pragma unroll
+                        for (int jj = 0; jj < NJ; ++jj)
+                            pv[u][v][jj] = __hip_atomic_load(reinterpret_cast<float *>(pbase(part) + poff(lo, int(i), v, jj)),
+                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+#pragma unroll
+                    for (int jj = 0; jj < NJ; ++jj) {
+                        float t = sum[v][jj];
+#pragma unroll
+                        for (int u = 0; u < 2; ++u) {
+                            const uint32_t part = p0 + uint32_t(u);
+                            const float val = part == kp ? slot[(v * NJ + jj) * kThreads + tid] : pv[u][v][jj];
+                            // the last arrival's order: (0 + part 0) + part 1 + ...
+                            t = part < kparts ? (part == 0 ? 0.f : t) + val : t;
+                        }
+                        sum[v][jj] = t;
+                    }
+            }
+            write_out(int(i), [&](int v, int jj) {
+                const float r = ACC == ACC_FP16 ? round_f16p(sum[v][jj]) : sum[v][jj];
+                return late ? __builtin_nanf("") : r;
+            });
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -699,6 +798,31 @@ GemmPlan plan_gemm(uint32_t cols, uint32_t rows, uint32_t batch, bool pair, cons
     return p;
 }
 
+// Workgroups of one instance the device holds at once, per device and instance.
+template <class K>
+uint64_t resident_wgs(K kernel) {
+    struct Entry {
+        const void *k;
+        int dev, n;
+    };
+    static Entry cache[64] = {};
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    const void *key = reinterpret_cast<const void *>(kernel);
+    for (Entry &e : cache)
+        if (e.k == key && e.dev == dev) return e.n > 0 ? uint64_t(e.n) : 0;
+    int wgs = 0, cus = 0, n = -1;  // unknown: never taken as room
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&wgs, kernel, kThreads, 0) == hipSuccess && wgs > 0 &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+        n = wgs * cus;
+    for (Entry &e : cache)
+        if (e.k == nullptr) {
+            e = Entry{key, dev, n};
+            break;
+        }
+    return n > 0 ? uint64_t(n) : 0;
+}
+
 template <int TYPE, int LAYOUT, bool PAIR>
 hipError_t launch_mode(int acc, const uint8_t *w, const uint8_t *up, const uint16_t *x, const uint16_t *xh,
                        void *out, uint32_t cols, uint32_t rows, uint32_t batch, const Workspace &ws,
@@ -707,12 +831,13 @@ hipError_t launch_mode(int acc, const uint8_t *w, const uint8_t *up, const uint1
     const dim3 grid(p.ntok * p.ncol * p.kparts), block(kThreads);
     const uint32_t wbytes = rows * (cols / kQK) * block_bytes(TYPE);
     float *partial = ws.partial + ws_offset;
-    if (acc == ACC_FP16)
-        gemm_kernel<TYPE, LAYOUT, ACC_FP16, PAIR><<<grid, block, 0, stream>>>(
-            w, up, x, xh, out, partial, ws.counters, cols, rows, batch, p.ntok, p.ncol, p.kparts, wbytes);
-    else
-        gemm_kernel<TYPE, LAYOUT, ACC_FP32, PAIR><<<grid, block, 0, stream>>>(
-            w, up, x, xh, out, partial, ws.counters, cols, rows, batch, p.ntok, p.ncol, p.kparts, wbytes);
+    const auto kernel = acc == ACC_FP16 ? &gemm_kernel<TYPE, LAYOUT, ACC_FP16, PAIR> : &gemm_kernel<TYPE, LAYOUT, ACC_FP32, PAIR>;
+    // the reduce-scatter needs every part of a tile running at once: the whole grid resident
+    uint32_t rs_spin = 0;
+    if (p.kparts > 1 && MI % p.kparts == 0 && ws.tune.gemm_rs != 0 && uint64_t(grid.x) <= resident_wgs(kernel))
+        rs_spin = ws.tune.gemm_rs > 1 ? uint32_t(ws.tune.gemm_rs) : 1u << 22;  // 2^22 polls of s_sleep 2: seconds
+    kernel<<<grid, block, 0, stream>>>(w, up, x, xh, out, partial, ws.counters, cols, rows, batch, p.ntok, p.ncol,
+                                       p.kparts, wbytes, rs_spin);
     return hipGetLastError();
 }
 
@@ -767,7 +892,7 @@ static void gemm_fp32_workspace_need(int type, int layout, uint32_t cols, uint32
     const GemmPlan p = plan_gemm(cols, rows, batch, pair, t);
     *floats = xs_floats(type, cols, batch) +
               (p.kparts > 1 ? size_t(p.kparts) * (pair ? 2 : 1) * (p.ntok * TT) * (p.ncol * (pair ? TC / 2 : TC)) : 0);
-    *counters = size_t(p.ntok) * p.ncol;
+    *counters = 2 * size_t(p.ntok) * p.ncol;  // arrivals; and departures of the reduce-scatter
 }
 
 hipError_t launch_gemm(int type, int layout, int acc, const uint8_t *w, const uint8_t *up, const uint16_t *x,

@@ -105,9 +105,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
     const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, const uint16_t *__restrict__ x,
     const uint16_t *__restrict__ xsums, void *__restrict__ out, float *__restrict__ partial,
     uint32_t *__restrict__ counters, uint32_t cols, uint32_t rows, uint32_t batch, uint32_t ntok_tiles,
-    uint32_t ncol_tiles, uint32_t kparts, uint32_t wbytes) {
+    uint32_t ncol_tiles, uint32_t kparts, uint32_t wbytes, uint32_t rs_spin) {
     __shared__ __attribute__((aligned(16))) u32x4 Xs[XBUF][TT * 8];
-    __shared__ uint32_t last_flag;
+    __shared__ uint32_t last_flag, late_flag;
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, hl = lane >> 5;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -376,6 +376,98 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
         return (uint32_t(i) * 32 + 8 * uint32_t(v >> 2) + uint32_t(v & 3)) * rstride + lo[j];
     };
     auto pbase = [&](uint32_t part) -> char * { return reinterpret_cast<char *>(partial + part * pstride); };  // uniform
+    if (rs_spin != 0) {
+        // Reduce-scatter (launched only when the whole grid fits on the device at once, so the
+        // kparts workgroups of a tile run together; kparts == MI): part kp owns token sub-tile
+        // kp of every wave.  Each part stores the sub-tiles it does not own, parks its own in
+        // LDS (the x buffers, free after the main loop), counts one arrival on written[tile]
+        // once its stores are acknowledged, waits until every part has, then adds the parts of
+        // its sub-tile in part order (its own from LDS) and writes it.  The wait is bounded: a
+        // part whose limit runs out writes its sub-tile as NaN.  The last part past the wait
+        // clears both counters.
+        const uint32_t ntiles = ntok_tiles * ncol_tiles;
+        uint32_t *written = counters + tile, *departed = counters + ntiles + tile;
+        float *slot = reinterpret_cast<float *>(&Xs[0][0]);
+        __syncthreads();  // every wave is past its last read of the x buffers
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+            if (uint32_t(i) == kp) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) slot[(v * NJ + j) * kThreads + tid] = acc[i][j][v];
+            } else {
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j)
+                        __hip_atomic_store(reinterpret_cast<float *>(pbase(kp) + poff(lane_off, i, v, j)), acc[i][j][v],
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __syncthreads();
+        if (tid == 0) {
+            __hip_atomic_fetch_add(written, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            uint32_t late = 0;
+            for (uint32_t it = 0; __hip_atomic_load(written, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < kparts;) {
+                __builtin_amdgcn_s_sleep(2);
+                if (++it >= rs_spin) {
+                    late = 1;
+                    break;
+                }
+            }
+            late_flag = late;
+            if (__hip_atomic_fetch_add(departed, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == kparts - 1) {
+                __hip_atomic_store(written, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(departed, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        __syncthreads();
+        const bool late = late_flag != 0;
+        float sum[16][NJ];
+        for (uint32_t p0 = 0; p0 < kparts; p0 += 2) {  // two parts per round trip
+            float pv[2][16][NJ];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                // this part's own slot holds no value for its sub-tile: read from LDS below
+                const uint32_t part = __builtin_elementwise_min(p0 + uint32_t(u), kparts - 1);
+                uint32_t lo[NJ];
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    lo[j] = lane_off[j];
+                    asm volatile("" : "+v"(lo[j]));
+                }
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j)
+                        pv[u][v][j] = __hip_atomic_load(reinterpret_cast<float *>(pbase(part) + poff(lo, int(kp), v, j)),
+                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    float t = sum[v][j];
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const uint32_t part = p0 + uint32_t(u);
+                        const float val = part == kp ? slot[(v * NJ + j) * kThreads + tid] : pv[u][v][j];
+                        // the last arrival's order: (0 + part 0) + part 1 + ...
+                        t = part < kparts ? (part == 0 ? 0.f : t) + val : t;
+                    }
+                    sum[v][j] = t;
+                }
+        }
+        write_out(int(kp), [&](int v, int j) {
+            const float r = ACC == ACC_FP16 ? round_f16p(sum[v][j]) : sum[v][j];
+            return late ? __builtin_nanf("") : r;
+        });
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -437,6 +529,28 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
     }
 }
 
+// Workgroups of one instance the device holds at once (two per CU), per device and instance.
+template <class K>
+uint64_t resident_wgs(K kernel) {
+    static int cache[64][4] = {};
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    const int slot = kernel == &gemm_reg_kernel<ACC_FP16, true>    ? 0
+                     : kernel == &gemm_reg_kernel<ACC_FP32, true>  ? 1
+                     : kernel == &gemm_reg_kernel<ACC_FP16, false> ? 2
+                                                                   : 3;
+    int &n = cache[dev & 63][slot];
+    if (n == 0) {
+        int wgs = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&wgs, kernel, kThreads, 0) != hipSuccess || wgs <= 0 ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            n = -1;  // unknown: never taken as room
+        else
+            n = wgs * cus;
+    }
+    return n > 0 ? uint64_t(n) : 0;
+}
+
 struct RegPlan {
     uint32_t ntok, ncol, kparts;
 };
@@ -462,7 +576,7 @@ void gemm_reg_workspace_need(uint32_t cols, uint32_t rows, uint32_t batch, bool 
                              size_t *part_floats, size_t *counters) {
     const RegPlan p = plan_reg(cols, rows, batch, pair, t);
     *part_floats = p.kparts > 1 ? size_t(p.kparts) * (pair ? 2 : 1) * (p.ntok * TT) * (p.ncol * (pair ? TC / 2 : TC)) : 0;
-    *counters = size_t(p.ntok) * p.ncol;
+    *counters = 2 * size_t(p.ntok) * p.ncol;  // written, then departed (reduce-scatter); the first alone otherwise
 }
 
 hipError_t launch_gemm_reg(int acc, const uint8_t *w, const uint8_t *up, const uint16_t *x, const uint16_t *xsums,
@@ -472,21 +586,15 @@ hipError_t launch_gemm_reg(int acc, const uint8_t *w, const uint8_t *up, const u
     const RegPlan p = plan_reg(cols, rows, batch, pair, t);
     const dim3 grid(p.ntok * p.ncol * p.kparts), block(kThreads);
     const uint32_t wbytes = rows * (cols / kQK) * kQ4Bytes;
-    if (pair) {
-        if (acc == ACC_FP16)
-            gemm_reg_kernel<ACC_FP16, true><<<grid, block, 0, stream>>>(w, up, x, xsums, out, partial, counters, cols, rows,
-                                                                        batch, p.ntok, p.ncol, p.kparts, wbytes);
-        else
-            gemm_reg_kernel<ACC_FP32, true><<<grid, block, 0, stream>>>(w, up, x, xsums, out, partial, counters, cols, rows,
-                                                                        batch, p.ntok, p.ncol, p.kparts, wbytes);
-    } else {
-        if (acc == ACC_FP16)
-            gemm_reg_kernel<ACC_FP16, false><<<grid, block, 0, stream>>>(w, w, x, xsums, out, partial, counters, cols, rows,
-                                                                         batch, p.ntok, p.ncol, p.kparts, wbytes);
-        else
-            gemm_reg_kernel<ACC_FP32, false><<<grid, block, 0, stream>>>(w, w, x, xsums, out, partial, counters, cols, rows,
-                                                                         batch, p.ntok, p.ncol, p.kparts, wbytes);
-    }
+    const auto kernel = pair ? (acc == ACC_FP16 ? &gemm_reg_kernel<ACC_FP16, true> : &gemm_reg_kernel<ACC_FP32, true>)
+                             : (acc == ACC_FP16 ? &gemm_reg_kernel<ACC_FP16, false> : &gemm_reg_kernel<ACC_FP32, false>);
+    // the reduce-scatter needs every part of a tile running at once (the whole grid resident) and
+    // one token sub-tile per part (its LDS slot)
+    uint32_t rs_spin = 0;
+    if (p.kparts == uint32_t(MI) && t.gemm_rs != 0 && uint64_t(grid.x) <= resident_wgs(kernel))
+        rs_spin = t.gemm_rs > 1 ? uint32_t(t.gemm_rs) : 1u << 22;  // 2^22 polls of s_sleep 2: seconds
+    kernel<<<grid, block, 0, stream>>>(w, pair ? up : w, x, xsums, out, partial, counters, cols, rows, batch, p.ntok,
+                                       p.ncol, p.kparts, wbytes, rs_spin);
     return hipGetLastError();
 }
 

@@ -139,43 +139,51 @@ def _down_case(qtype, batch, seed):
     return cols, rows, w, xd
 
 
-def _run_down(ctx, qtype, cols, rows, batch, w, xd):
+def _run_down(ctx, qtype, cols, rows, batch, w, xd, fast=True):
     y = torch.full((batch, rows), float("nan"), dtype=torch.float32, device="cuda")
-    ctx.ffn_down(w, qtype, N.CDNA4, cols, rows, batch, xd, y, half_input=True, fast_swa=True)
+    ctx.ffn_down(w, qtype, N.CDNA4, cols, rows, batch, xd, y, half_input=True, fast_swa=fast)
     torch.cuda.synchronize()
     return y.cpu().numpy()
+
+
+MODES = {"fp16": True, "fp32": False}
 
 
 @pytest.mark.parametrize("kparts", [0, 2, 8], ids=["plan", "split2", "split8"])
 @pytest.mark.parametrize("batch", [1024, 300])
 @pytest.mark.parametrize("qtype", [N.Q4_K, N.Q6_K], ids=["q4k", "q6k"])
-def test_split_k_reduce_scatter_equals_last_arrival(ctx, tune, qtype, batch, kparts):
-    """The FP16-mode down projection (3840 x 15360, CDNA4) finishes its split-K tiles either by
-    a reduce-scatter (every part adds the parts of its own token sub-tiles; the default when the
-    grid fits the device at once) or by the last part to arrive (tuning key gemm_rs 0).  Both add
-    the same fp32 parts in part order, so the outputs are equal bit for bit."""
+@pytest.mark.parametrize("mode", list(MODES))
+def test_split_k_reduce_scatter_equals_last_arrival(ctx, tune, mode, qtype, batch, kparts):
+    """The down projection (3840 x 15360, CDNA4), in either accumulation mode, finishes its
+    split-K tiles either by a reduce-scatter (every part adds the parts of its own token
+    sub-tiles; the default when the grid fits the device at once and, in the FP32 mode, when
+    the parts number as many as a wave's token sub-tiles) or by the last part to arrive
+    (tuning key gemm_rs 0).  Both add the same fp32 parts in part order, so the outputs are
+    equal bit for bit."""
     if kparts:
         tune("gemm_kparts", kparts)
     cols, rows, w, xd = _down_case(qtype, batch, 0xD0 + batch)
-    a = _run_down(ctx, qtype, cols, rows, batch, w, xd)
+    a = _run_down(ctx, qtype, cols, rows, batch, w, xd, MODES[mode])
     tune("gemm_rs", 0)
-    b = _run_down(ctx, qtype, cols, rows, batch, w, xd)
+    b = _run_down(ctx, qtype, cols, rows, batch, w, xd, MODES[mode])
     assert np.isfinite(a).all()
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-def test_split_k_reduce_scatter_bounded_wait(ctx, tune):
+@pytest.mark.parametrize("qtype", [N.Q4_K, N.Q6_K], ids=["q4k", "q6k"])
+@pytest.mark.parametrize("mode", list(MODES))
+def test_split_k_reduce_scatter_bounded_wait(ctx, tune, mode, qtype):
     """The reduce-scatter's wait for the other parts is bounded.  Forced down to two polls from
     the host (every wave still exits normally), a part whose wait ran out writes its token
     sub-tiles (32 tokens each) as NaN and every other sub-tile is the normal result; the next
     launch with the default bound is whole again (the last part clears the counters)."""
-    qtype, batch = N.Q6_K, 1024
+    batch = 1024
     cols, rows, w, xd = _down_case(qtype, batch, 0xE0)
-    want = _run_down(ctx, qtype, cols, rows, batch, w, xd)
+    want = _run_down(ctx, qtype, cols, rows, batch, w, xd, MODES[mode])
     tune("gemm_rs", 2)
-    got = _run_down(ctx, qtype, cols, rows, batch, w, xd)
+    got = _run_down(ctx, qtype, cols, rows, batch, w, xd, MODES[mode])
     tune("gemm_rs", 1)
-    again = _run_down(ctx, qtype, cols, rows, batch, w, xd)
+    again = _run_down(ctx, qtype, cols, rows, batch, w, xd, MODES[mode])
     blocks = got.reshape(batch // 32, 32, rows // 256, 256).transpose(0, 2, 1, 3)
     ref = want.reshape(batch // 32, 32, rows // 256, 256).transpose(0, 2, 1, 3)
     nan_blocks = 0
