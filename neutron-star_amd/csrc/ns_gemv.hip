@@ -198,6 +198,86 @@ __device__ __forceinline__ float q6_dot(const u32x4 (&c)[kQ6Chunks], uint32_t db
     return d * s;
 }
 
+// q6_dot in two halves, for a caller that holds the block before x is known.  q6_merge6
+// forms the 256 six-bit values, one per byte, in 64 dwords: m[4*((2h + t)*4 + u) + j] holds
+// quarter j of (h, t, u) for l = 4u .. 4u+3 (byte k = element l + k, the bytes whose two
+// 2-bit-and-nibble halves q6_dot assembles as e_j).  q6_dot_merged then takes each e_j as
+// one byte permute (bytes odd and 2 + odd to the two fp16 halves: v * 2^-24) and issues
+// q6_dot's FMAs in q6_dot's order.  Quarters 2 and 3 carry 2^-24 here instead of 2^-20: every
+// product and partial sum of their groups is the same value times 2^-4, which the final factor
+// 2^24 (instead of 2^20) undoes exactly, so the result equals q6_dot's bit for bit.
+__device__ __forceinline__ uint32_t q6_merge6(uint32_t ql, uint32_t qh, int j) {
+    const uint32_t lo = (j >= 2 ? ql >> 4 : ql) & 0x0F0F0F0Fu;
+    const uint32_t hb = j == 0 ? (qh << 4) : j == 1 ? (qh << 2) : j == 2 ? qh : (qh >> 2);
+    return lo | (hb & 0x30303030u);
+}
+
+__device__ __forceinline__ void q6_merge_block(const u32x4 (&c)[kQ6Chunks], uint32_t (&m)[64]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t a = comp(c[4 * h + t], u), b = comp(c[4 * h + 2 + t], u);
+                const uint32_t hq = comp(c[8 + 2 * h + t], u);
+                uint32_t *mm = m + 4 * ((2 * h + t) * 4 + u);
+                mm[0] = q6_merge6(a, hq, 0);
+                mm[1] = q6_merge6(b, hq, 1);
+                mm[2] = q6_merge6(a, hq, 2);
+                mm[3] = q6_merge6(b, hq, 3);
+            }
+}
+
+__device__ __forceinline__ float q6_dot_merged(const uint32_t (&m)[64], const u32x4 &scales, uint32_t dbits,
+                                               const float *__restrict__ xb, const float (&xs)[16]) {
+    float s = 0.f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        // half h's eight groups (i = 8h .. 8h+7) are finished before half h+1 starts: s adds
+        // the groups in q6_dot's order, and only eight accumulators are live
+        float A[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) A[i] = 0.f;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                // the x reads of one (t, u) step are not hoisted above the previous step: the
+                // 256 broadcast values would otherwise fill the register budget
+                __builtin_amdgcn_sched_barrier(0);
+                const uint32_t *mm = m + 4 * ((2 * h + t) * 4 + u);
+                const float *x0 = xb + 128 * h + 16 * t + 4 * u;
+#pragma unroll
+                for (int odd = 0; odd < 2; ++odd) {
+                    // bytes odd and 2 + odd into the low bytes of the two halves, zero above
+                    const uint32_t sel = odd ? 0x0C030C01u : 0x0C020C00u;
+                    const uint32_t e0 = __builtin_amdgcn_perm(0u, mm[0], sel);
+                    const uint32_t e1 = __builtin_amdgcn_perm(0u, mm[1], sel);
+                    const uint32_t e2 = __builtin_amdgcn_perm(0u, mm[2], sel);
+                    const uint32_t e3 = __builtin_amdgcn_perm(0u, mm[3], sel);
+                    const float *xo = x0 + odd;
+                    float &g0 = A[0 + t], &g1 = A[2 + t], &g2 = A[4 + t], &g3 = A[6 + t];
+                    g0 = __builtin_fmaf(lo_half(e0), xo[0], g0);
+                    g0 = __builtin_fmaf(hi_half(e0), xo[2], g0);
+                    g1 = __builtin_fmaf(lo_half(e1), xo[32], g1);
+                    g1 = __builtin_fmaf(hi_half(e1), xo[34], g1);
+                    g2 = __builtin_fmaf(lo_half(e2), xo[64], g2);
+                    g2 = __builtin_fmaf(hi_half(e2), xo[66], g2);
+                    g3 = __builtin_fmaf(lo_half(e3), xo[96], g3);
+                    g3 = __builtin_fmaf(hi_half(e3), xo[98], g3);
+                }
+            }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int i = 8 * h + k;
+            const float sc = float(int8_t(byte_of(comp(scales, i >> 2), i & 3)));
+            s = __builtin_fmaf(sc, __builtin_fmaf(A[k], 16777216.0f, -32.0f * xs[i]), s);
+        }
+    }
+    return lo_half(dbits) * s;
+}
+
 // ---- several tokens (the batch 2-4 regime) -------------------------------------
 //
 // The block is unpacked once and multiplies NT token vectors.  Per token the FMA
@@ -340,15 +420,24 @@ __device__ __forceinline__ void group_sums_x(const void *__restrict__ xb, uint32
         xs[g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), g * (GROUP / 4)));
 }
 
+// Lane exchange by DPP (no address registers, no LDS): 0xB1 and 0x4E are quad_perm [1,0,3,2]
+// and [2,3,0,1] (lane ^ 1, lane ^ 2), 0x141 row_half_mirror (lane i of 8 takes lane 7 - i).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
 // Sums of x over the block's groups of 32 (Q4_K, 8 values) or 16 (Q6_K, 16
 // values), returned wave-uniform.  Each lane adds 4 values; the groups are
-// completed with cross-lane exchanges and read back with readlane.
+// completed with cross-lane exchanges and read back with readlane.  After the
+// two quad steps every lane of a quad holds the quad's sum, so the mirrored lane
+// of the other quad (lane 7 - i) holds the value lane i ^ 4 holds.
 template <int GROUP>
 __device__ __forceinline__ void group_sums_of(const float4 &v, float *xs) {
     float s = (v.x + v.y) + (v.z + v.w);
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    if constexpr (GROUP == 32) s += __shfl_xor(s, 4);
+    s += dpp_f<0xB1>(s);
+    s += dpp_f<0x4E>(s);
+    if constexpr (GROUP == 32) s += dpp_f<0x141>(s);
 #pragma unroll
     for (int g = 0; g < 256 / GROUP; ++g)
         xs[g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), g * (GROUP / 4)));
@@ -1303,12 +1392,25 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
     uint32_t dbits = 0;
     const auto load_down = [&] {
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        if constexpr (DTYPE == Q4_K) q4_load<CDNA4>(wd, lane, 0, dslab, b, nbd, c);
-        else q6_load<CDNA4>(wd, lane, 0, dslab, b, nbd, c, dbits);
+        if constexpr (DTYPE == Q4_K) {
+            q4_load<CDNA4>(wd, lane, 0, dslab, b, nbd, c);
+        } else {
+            // the 13 chunks only: d is read with h (a register less across the wait)
+            const u32x4 *p = reinterpret_cast<const u32x4 *>(wd + region_offset(Q6_K, dslab, b, nbd)) + lane;
+#pragma unroll
+            for (int i = 0; i < int(kQ6Chunks); ++i) c[i] = __builtin_nontemporal_load(p + i * 64);
+        }
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    };
+    // Q6_K: the six-bit values are merged while the wave waits for h (q6_merge_block), so only
+    // the byte permutes and the FMAs of q6_dot remain once h is complete
+    uint32_t m6[64];
+    const auto merge_down = [&] {
+        if constexpr (DTYPE == Q6_K) q6_merge_block(c, m6);
     };
     if (wave != 0) load_down();
     lds_barrier();
+    if (wave != 0) merge_down();
     if (wave == 0) {
         float gs = 0.f, us = 0.f;
         for (uint32_t v = 0; v < W; ++v) {
@@ -1329,6 +1431,7 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         if (lane == 0) __hip_atomic_fetch_add(&ready[kq * kCtrStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         load_down();
+        merge_down();
         // ---- 3. wait for the DS gate/up slabs of part kq ----
         if (lane == 0) {
             uint32_t it = 0;
@@ -1343,12 +1446,18 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
     }
     // wave 0's reads of lds_part end before any wave writes it again below
     lds_barrier();
+    if constexpr (DTYPE == Q6_K)
+        dbits = reinterpret_cast<const uint16_t *>(wd + region_offset(Q6_K, dslab, b, nbd) + kQ6Chunks * 1024)[lane];
     const float *hb = h + size_t(b) * kQK + 4 * lane;
     const float4 hv{__hip_atomic_load(hb + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
                     __hip_atomic_load(hb + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
                     __hip_atomic_load(hb + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
                     __hip_atomic_load(hb + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)};
-    reinterpret_cast<float4 *>(xw)[lane] = hv;
+    // lane-derived LDS addresses are formed again here from an opaque copy of the lane: kept
+    // from the start, they would be live across the wait (spilled at four waves per SIMD)
+    uint32_t lane_b = lane;
+    if constexpr (DTYPE == Q6_K) asm volatile("" : "+v"(lane_b));
+    reinterpret_cast<float4 *>(xw)[lane_b] = hv;
     float acc;
     if constexpr (DTYPE == Q4_K) {
         const u32x4(&cc)[1][kQ4Chunks] = reinterpret_cast<const u32x4(&)[1][kQ4Chunks]>(c);
@@ -1359,9 +1468,9 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
     } else {
         float xs[16];
         group_sums_of<16>(hv, xs);
-        acc = q6_dot(c, dbits, xw, xs);
+        acc = q6_dot_merged(m6, c[12], dbits, xw, xs);
     }
-    lds_part[wave][0][lane] = acc;
+    lds_part[wave][0][lane_b] = acc;
     __syncthreads();
     if (wave == 0) {
         float r0 = 0.f;
