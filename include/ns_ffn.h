@@ -107,7 +107,11 @@ int ns_ctx_set_tuning(ns_ctx *ctx, const char *key, int value);
  *   batch  > 4, half_input != 0 -> dequant-into-LDS MFMA GEMM, FP32 accumulation (any layout:
  *                                  the reference's swizzled row-major kernels, metal:263-301,
  *                                  432-478, serve attention tensors that stay row-major).
- *   batch  > 4, fp32 input      -> one GEMV per token.
+ *   batch  > 4, fp32 input      -> the same GEMM on x rounded to fp16 (round to nearest even),
+ *                                  as the reference's tile loader converts fp32 x to half
+ *                                  (metal:235, gemma_q{4,6}k_mma_swizzled, mm:274); the fp16
+ *                                  copy lives in the context (grown like the workspace, refused
+ *                                  under stream capture); fp32 input must be 16-byte aligned.
  * `in` is fp32 [batch][cols] or, with half_input, fp16 bits [batch][cols]; out fp32 [batch][rows]. */
 int ns_matmul(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, uint32_t rows,
               uint32_t batch, const void *in, int half_input, float *out, void *stream);
@@ -118,7 +122,8 @@ int ns_matmul(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, u
  * reductions use a static device scratch array of 16 MiB of parts and 65,536 counters that
  * each GPU holds until the process ends; a shape that needs more fails with
  * NS_ERR_UNSUPPORTED (every decode GEMV and small-batch shape of the reference model fits;
- * large prefill GEMMs do not).  fp32 input above batch 4 is refused.  Calls that overlap on
+ * large prefill GEMMs do not).  fp32 input above batch 4 is refused (its fp16 copy would need
+ * a buffer).  Calls that overlap on
  * one GPU share the array and race: order them (one stream).  Allocates nothing, never
  * synchronises, and may be captured into a graph. */
 int ns_matmul_noalloc(const void *w, int type, int layout, uint32_t cols, uint32_t rows, uint32_t batch,

@@ -15,6 +15,9 @@
 struct ns_ctx {
     int device = 0;
     ns::Workspace ws;
+    // fp16 copy of an fp32 input for the GEMM (matmul above batch 4 with fp32 input)
+    uint16_t *xh = nullptr;
+    size_t xh_count = 0;
     // Buffers replaced by workspace growth.  Work queued earlier, or a graph
     // captured earlier, may still use them, so they live until ns_ctx_destroy.
     std::vector<void *> retired;
@@ -85,6 +88,24 @@ int ensure_ws(ns_ctx *ctx, size_t partial_floats, size_t counters, hipStream_t s
         ctx->ws.counters = c;
         ctx->ws.counter_count = counters;
     }
+    return NS_OK;
+}
+
+// Makes the context's fp16 input buffer hold at least n values, on the same terms as
+// ensure_ws (growth retires the old buffer and is refused during stream capture).
+int ensure_xh(ns_ctx *ctx, size_t n, hipStream_t s) {
+    if (n <= ctx->xh_count) return NS_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (s && hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+        return fail(NS_ERR_UNSUPPORTED, "input buffer growth during stream capture: run the shape once before capturing");
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return hip_fail(e, "input buffer growth");
+    uint16_t *p = nullptr;
+    e = hipMalloc(reinterpret_cast<void **>(&p), n * sizeof(uint16_t));
+    if (e != hipSuccess) return hip_fail(e, "input buffer allocation");
+    if (ctx->xh) ctx->retired.push_back(ctx->xh);
+    ctx->xh = p;
+    ctx->xh_count = n;
     return NS_OK;
 }
 
@@ -221,6 +242,7 @@ extern "C" int ns_ctx_destroy(ns_ctx *ctx) {
     (void)hipDeviceSynchronize();
     if (ctx->ws.partial) (void)hipFree(ctx->ws.partial);
     if (ctx->ws.counters) (void)hipFree(ctx->ws.counters);
+    if (ctx->xh) (void)hipFree(ctx->xh);
     for (void *p : ctx->retired) (void)hipFree(p);
     delete ctx;
     return NS_OK;
@@ -232,8 +254,8 @@ extern "C" int ns_matmul(ns_ctx *ctx, const void *w, int type, int layout, uint3
     if (int rc = check_tensor("ns_matmul", w, type, layout, cols, rows)) return rc;
     if (!in || !out || batch == 0) return fail(NS_ERR_ARG, "ns_matmul: null input/output or zero batch");
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    // mm:269-275: batch 2-4 -> the small-batch kernels (fp32 or fp16 input); batch > 4 with
-    // fp16 input -> the MMA (prefill) GEMM
+    // mm:269-275: batch 2-4 -> the small-batch kernels (fp32 or fp16 input); batch > 4 -> the
+    // MMA (prefill) GEMM
     if (batch >= 2 && batch <= 4)
         return gemv_mt(ctx, "ns_matmul", type, layout, w, nullptr, in, half_input != 0, batch, out, cols, rows, s);
     if (half_input && batch > 1)
@@ -241,11 +263,16 @@ extern "C" int ns_matmul(ns_ctx *ctx, const void *w, int type, int layout, uint3
                     cols, rows, batch, s);
     if (half_input) return fail(NS_ERR_UNSUPPORTED, "ns_matmul: fp16 input at batch 1 is not a reference regime");
     const auto *x = static_cast<const float *>(in);
-    for (uint32_t t = 0; t < batch; ++t)
-        if (int rc = gemv(ctx, "ns_matmul", type, layout, w, nullptr, x + size_t(t) * cols, out + size_t(t) * rows,
-                          cols, rows, s))
-            return rc;
-    return NS_OK;
+    if (batch == 1) return gemv(ctx, "ns_matmul", type, layout, w, nullptr, x, out, cols, rows, s);
+    // mm:274: fp32 input above batch 4 takes the MMA GEMM too, whose tile loader rounds each x
+    // value to half (metal:235): x to fp16 (round to nearest even), then the prefill GEMM in
+    // the FP32 mode
+    if (reinterpret_cast<uintptr_t>(x) % 16) return fail(NS_ERR_ARG, "ns_matmul: fp32 input must be 16-byte aligned");
+    const size_t n = size_t(batch) * cols;
+    if (int rc = ensure_xh(ctx, n, s)) return rc;
+    const hipError_t e = launch_f32_to_f16(x, ctx->xh, n, s);
+    if (e != hipSuccess) return hip_fail(e, "ns_matmul");
+    return gemm(ctx, "ns_matmul", type, layout, ACC_FP32, w, nullptr, ctx->xh, out, cols, rows, batch, s);
 }
 
 extern "C" int ns_gate_up_geglu_decode(ns_ctx *ctx, const void *wg, const void *wu, int layout, uint32_t cols,

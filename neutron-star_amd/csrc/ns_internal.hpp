@@ -129,6 +129,9 @@ hipError_t launch_rmsnorm(const float *x, const float *w, const float *residual,
                           const float *next_w, uint32_t rows, uint32_t width, float eps, void *y, bool half_y,
                           void *next, bool half_next, hipStream_t stream);
 
+// y[i] = fp16(x[i]), round to nearest even; x 16-byte and y 8-byte aligned.
+hipError_t launch_f32_to_f16(const float *x, uint16_t *y, size_t n, hipStream_t stream);
+
 // out[t][i] = scale * W[ids[t]][i] (fp32 values as quant.cpp; NaN rows for ids out of range).
 hipError_t launch_embedding(int type, int layout, const uint8_t *w, uint32_t cols, uint32_t rows, const int32_t *ids,
                             uint32_t batch, float scale, float *out, hipStream_t stream);

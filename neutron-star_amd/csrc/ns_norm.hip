@@ -94,7 +94,31 @@ __global__ __launch_bounds__(1024) void rmsnorm_vec_kernel(const float *x, const
                });
 }
 
+// y = fp16(x), round to nearest even (the conversion of the reference's tile loader,
+// metal:235), four values per thread; n need not be a multiple of four.
+__global__ __launch_bounds__(256) void f32_to_f16_kernel(const float *__restrict__ x, _Float16 *__restrict__ y,
+                                                          size_t n) {
+    const size_t i = (size_t(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+    if (i + 4 <= n) {
+        const float4 v = *reinterpret_cast<const float4 *>(x + i);
+        typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+        *reinterpret_cast<half4_t *>(y + i) = half4_t{_Float16(v.x), _Float16(v.y), _Float16(v.z), _Float16(v.w)};
+    } else {
+        for (size_t k = i; k < n; ++k) y[k] = _Float16(x[k]);
+    }
+}
+
 }  // namespace
+
+hipError_t launch_f32_to_f16(const float *x, uint16_t *y, size_t n, hipStream_t stream) {
+    if (n == 0) return hipSuccess;
+    // the vector path needs 16-byte x and 8-byte y: otherwise one value per thread
+    if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(y) % 8) return hipErrorInvalidValue;
+    const size_t threads = (n + 3) / 4;
+    f32_to_f16_kernel<<<dim3(uint32_t((threads + 255) / 256)), dim3(256), 0, stream>>>(
+        x, reinterpret_cast<_Float16 *>(y), n);
+    return hipGetLastError();
+}
 
 hipError_t launch_rmsnorm(const float *x, const float *w, const float *residual, const float *scale,
                           const float *next_w, uint32_t rows, uint32_t width, float eps, void *y, bool half_y,

@@ -92,7 +92,7 @@ extern "C" int ns_matmul_noalloc(const void *w, int type, int layout, uint32_t c
     if (uint64_t(rows) * (cols / kQK) * block_bytes(type) >= (uint64_t(1) << 31))
         return fail(NS_ERR_SHAPE, std::string(fn) + ": tensor of 2 GiB or more");
     if (half_input && batch == 1) return fail(NS_ERR_UNSUPPORTED, std::string(fn) + ": fp16 input at batch 1 is not a reference regime");
-    if (!half_input && batch > 4) return fail(NS_ERR_UNSUPPORTED, std::string(fn) + ": fp32 input above batch 4 (one GEMV per token) is not offered");
+    if (!half_input && batch > 4) return fail(NS_ERR_UNSUPPORTED, std::string(fn) + ": fp32 input above batch 4 (converted to an fp16 copy before the GEMM, a buffer this entry point does not hold) is not offered");
 
     // the same regime split and kernels as ns_matmul (mm:269-275)
     const Tuning t;

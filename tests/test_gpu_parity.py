@@ -348,6 +348,28 @@ def _row_slice(host, qtype, cols, r0, nrows):
     return np.ascontiguousarray(host[r0 * bpr:(r0 + nrows) * bpr])
 
 
+@pytest.mark.parametrize("layout", [N.CDNA4, N.ROW_MAJOR], ids=LNAME.get)
+@pytest.mark.parametrize("qtype", [N.Q6_K, N.Q4_K], ids=["q6k", "q4k"])
+@pytest.mark.parametrize("batch", [5, 64, 300])
+def test_matmul_fp32_input_above_batch4(ctx, batch, qtype, layout):
+    """mm:274: fp32 input above batch 4 takes the MMA GEMM, whose tile loader rounds each x value
+    to half (metal:235).  The result equals the fp16-input call on x rounded to nearest even (numpy's
+    float16 conversion) bit for bit, and is within the FP32 bar of the oracle's GEMM on those
+    values."""
+    cols, rows = 1024, 320
+    hw, w = weights(qtype, 81 + batch, rows, cols, layout)
+    x = N.synth_normal_f32(82 + batch, batch * cols).reshape(batch, cols)
+    xh = x.astype(np.float16)
+    y32 = torch.full((batch, rows), float("nan"), dtype=torch.float32, device="cuda")
+    y16 = torch.full((batch, rows), float("nan"), dtype=torch.float32, device="cuda")
+    ctx.matmul(w, qtype, layout, cols, rows, batch, torch.from_numpy(x).cuda(), y32)
+    ctx.matmul(w, qtype, layout, cols, rows, batch, dev_u16(xh.view(np.uint16)), y16, half_input=True)
+    torch.cuda.synchronize()
+    got = y32.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), y16.cpu().numpy().view(np.uint32))
+    assert rel_err(got, O.gemm(qtype, O.ROW_MAJOR, hw, cols, rows, batch, xh.view(np.uint16), 0)) <= TOL32
+
+
 @pytest.mark.parametrize("acc", [N.ACC_FP32, N.ACC_FP16], ids=["fp32acc", "fp16acc"])
 def test_prefill_ffn_full_size(ctx, acc):
     """Config 3 at full size (batch 1024, 3840 -> 15360 -> 3840).  The GPU runs
