@@ -831,7 +831,11 @@ hipError_t launch_mode(int acc, const uint8_t *w, const uint8_t *up, const uint1
     const dim3 grid(p.ntok * p.ncol * p.kparts), block(kThreads);
     const uint32_t wbytes = rows * (cols / kQK) * block_bytes(TYPE);
     float *partial = ws.partial + ws_offset;
-    const auto kernel = acc == ACC_FP16 ? &gemm_kernel<TYPE, LAYOUT, ACC_FP16, PAIR> : &gemm_kernel<TYPE, LAYOUT, ACC_FP32, PAIR>;
+    // the FP16 mode on the CDNA4 layout runs ns_gemm_f16.hip: no FP16 instance is built for it
+    constexpr bool kHasFp16 = LAYOUT != CDNA4;
+    if (!kHasFp16 && acc == ACC_FP16) return hipErrorInvalidValue;
+    const auto kernel = acc == ACC_FP16 ? &gemm_kernel<TYPE, LAYOUT, kHasFp16 ? ACC_FP16 : ACC_FP32, PAIR>
+                                        : &gemm_kernel<TYPE, LAYOUT, ACC_FP32, PAIR>;
     // the reduce-scatter needs every part of a tile running at once: the whole grid resident
     uint32_t rs_spin = 0;
     if (p.kparts > 1 && MI % p.kparts == 0 && ws.tune.gemm_rs != 0 && uint64_t(grid.x) <= resident_wgs(kernel))
@@ -909,9 +913,8 @@ hipError_t launch_gemm(int type, int layout, int acc, const uint8_t *w, const ui
         if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     }
     const size_t off = xs_floats(type, cols, batch);
-    if (use_gemm_reg(type, layout, ws.tune))
-        return launch_gemm_reg(acc, w, up, x, xh, out, cols, rows, batch, ws.partial + off, ws.counters, ws.tune,
-                               stream);
+    if (use_gemm_reg(type, layout, ws.tune))  // CDNA4 and FP32 mode: the FP16 mode returned above
+        return launch_gemm_reg(w, up, x, xh, out, cols, rows, batch, ws.partial + off, ws.counters, ws.tune, stream);
     if (up) return launch_layout<Q4_K, true>(layout, acc, w, up, x, xh, out, cols, rows, batch, ws, off, stream);
     if (type == Q4_K)
         return launch_layout<Q4_K, false>(layout, acc, w, nullptr, x, xh, out, cols, rows, batch, ws, off, stream);

@@ -25,7 +25,8 @@
 // accumulator holds S / E with E = e * 2^14 per column and super-block; the
 // Q4_K min term is two extra MFMAs per super-block over the group sums of x
 // (hi + lo fp16 planes; the min factors as fp16 hi + lo), and entering a new super-block rescales the
-// accumulator by E_prev / E_cur (FP16 mode: rounds S to fp16 precision there).
+// accumulator by E_prev / E_cur.  FP32 mode only: the FP16 mode on this layout runs
+// ns_gemm_f16.hip.
 //
 // Tiling: a workgroup of 4 waves computes 128 tokens x 256 B columns; each
 // wave owns all 128 tokens (4 MFMA tiles) and 64 columns (2 tiles): for PAIR
@@ -61,12 +62,6 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes) {
 __device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, int(off), 0, 0); }
 __device__ __forceinline__ u32x2 bload8(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b64(r, int(off), 0, 0); }
 
-__device__ __forceinline__ float round_f16p(float v) {
-    uint32_t b = __builtin_bit_cast(uint32_t, v);
-    b = (b + 0x0fffu + ((b >> 13) & 1u)) & 0xffffe000u;
-    return __builtin_bit_cast(float, b);
-}
-
 // Raw bytes of one column for one k step: qs bytes 8*hl..8*hl+7 of chunks
 // 1+2p and 2+2p, and the block header (d, dmin, scales).
 struct Raw {
@@ -100,7 +95,7 @@ __device__ __forceinline__ void decode8(u32x2 w, half2_t slo, half2_t shi, half8
     hi = __builtin_bit_cast(half8_t, H);
 }
 
-template <int ACC, bool PAIR>
+template <bool PAIR>
 __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
     const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, const uint16_t *__restrict__ x,
     const uint16_t *__restrict__ xsums, void *__restrict__ out, float *__restrict__ partial,
@@ -261,10 +256,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
 #pragma unroll
                     for (int i = 0; i < MI; ++i)
 #pragma unroll
-                        for (int v = 0; v < 16; ++v) {
-                            if constexpr (ACC == ACC_FP16) acc[i][j][v] = round_f16p(acc[i][j][v] * Eprev[j]) * rinv;
-                            else acc[i][j][v] *= r;
-                        }
+                        for (int v = 0; v < 16; ++v) acc[i][j][v] *= r;
                 }
             }
 
@@ -315,10 +307,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
 #pragma unroll
         for (int i = 0; i < MI; ++i)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                acc[i][j][v] *= Ecur[j];
-                if constexpr (ACC == ACC_FP16) acc[i][j][v] = round_f16p(acc[i][j][v]);
-            }
+            for (int v = 0; v < 16; ++v) acc[i][j][v] *= Ecur[j];
     auto tok_of = [&](int i, int v) -> uint32_t {
         return t0 + uint32_t(i) * 32 + 8 * uint32_t(v >> 2) + 4 * hl + uint32_t(v & 3);
     };
@@ -463,8 +452,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
                 }
         }
         write_out(int(kp), [&](int v, int j) {
-            const float r = ACC == ACC_FP16 ? round_f16p(sum[v][j]) : sum[v][j];
-            return late ? __builtin_nanf("") : r;
+            return late ? __builtin_nanf("") : sum[v][j];
         });
         return;
     }
@@ -525,20 +513,17 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
         }
 #pragma unroll
         for (int ii = 0; ii < 2; ++ii)
-            write_out(i0 + ii, [&](int v, int j) { return ACC == ACC_FP16 ? round_f16p(sum[ii][v][j]) : sum[ii][v][j]; });
+            write_out(i0 + ii, [&](int v, int j) { return sum[ii][v][j]; });
     }
 }
 
 // Workgroups of one instance the device holds at once (two per CU), per device and instance.
 template <class K>
 uint64_t resident_wgs(K kernel) {
-    static int cache[64][4] = {};
+    static int cache[64][2] = {};
     int dev = 0;
     (void)hipGetDevice(&dev);
-    const int slot = kernel == &gemm_reg_kernel<ACC_FP16, true>    ? 0
-                     : kernel == &gemm_reg_kernel<ACC_FP32, true>  ? 1
-                     : kernel == &gemm_reg_kernel<ACC_FP16, false> ? 2
-                                                                   : 3;
+    const int slot = kernel == &gemm_reg_kernel<true> ? 0 : 1;
     int &n = cache[dev & 63][slot];
     if (n == 0) {
         int wgs = 0, cus = 0;
@@ -579,15 +564,14 @@ void gemm_reg_workspace_need(uint32_t cols, uint32_t rows, uint32_t batch, bool 
     *counters = 2 * size_t(p.ntok) * p.ncol;  // written, then departed (reduce-scatter); the first alone otherwise
 }
 
-hipError_t launch_gemm_reg(int acc, const uint8_t *w, const uint8_t *up, const uint16_t *x, const uint16_t *xsums,
+hipError_t launch_gemm_reg(const uint8_t *w, const uint8_t *up, const uint16_t *x, const uint16_t *xsums,
                            void *out, uint32_t cols, uint32_t rows, uint32_t batch, float *partial,
                            uint32_t *counters, const Tuning &t, hipStream_t stream) {
     const bool pair = up != nullptr;
     const RegPlan p = plan_reg(cols, rows, batch, pair, t);
     const dim3 grid(p.ntok * p.ncol * p.kparts), block(kThreads);
     const uint32_t wbytes = rows * (cols / kQK) * kQ4Bytes;
-    const auto kernel = pair ? (acc == ACC_FP16 ? &gemm_reg_kernel<ACC_FP16, true> : &gemm_reg_kernel<ACC_FP32, true>)
-                             : (acc == ACC_FP16 ? &gemm_reg_kernel<ACC_FP16, false> : &gemm_reg_kernel<ACC_FP32, false>);
+    const auto kernel = pair ? &gemm_reg_kernel<true> : &gemm_reg_kernel<false>;
     // the reduce-scatter needs every part of a tile running at once (the whole grid resident) and
     // one token sub-tile per part (its LDS slot)
     uint32_t rs_spin = 0;

@@ -92,12 +92,12 @@ void gemv_mt_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, 
 void gemm_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, uint32_t batch, bool pair,
                          const Tuning &t, size_t *floats, size_t *counters);
 
-// The Q4_K CDNA4 prefill GEMM with register-resident weight fragments
+// The Q4_K CDNA4 prefill GEMM with register-resident weight fragments, FP32 mode
 // (ns_gemm_reg.hip): split-K parts it needs, and the launch.  xsums: the two
 // fp16 planes of x group sums; partial: the split-K parts.
 void gemm_reg_workspace_need(uint32_t cols, uint32_t rows, uint32_t batch, bool pair, const Tuning &t,
                              size_t *part_floats, size_t *counters);
-hipError_t launch_gemm_reg(int acc, const uint8_t *w, const uint8_t *up, const uint16_t *x, const uint16_t *xsums,
+hipError_t launch_gemm_reg(const uint8_t *w, const uint8_t *up, const uint16_t *x, const uint16_t *xsums,
                            void *out, uint32_t cols, uint32_t rows, uint32_t batch, float *partial,
                            uint32_t *counters, const Tuning &t, hipStream_t stream);
 
