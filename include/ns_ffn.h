@@ -19,7 +19,8 @@
  *     the message of the last failure on the calling thread.  The C++ wrapper
  *     (neutron-star_amd/host/ffn_path.hpp) rethrows it as std::runtime_error,
  *     which is how the reference reports failures (mm:231-243).
- *   - A context owns the workspace used for split reductions.  Calls that share
+ *   - A context owns the workspace used for split reductions (and the fp16 copy
+ *     of an fp32 matmul input above batch 4).  Calls that share
  *     one context must be ordered (one stream, or synchronised); the reference
  *     serialises all GPU work the same way (mm:137).
  */
