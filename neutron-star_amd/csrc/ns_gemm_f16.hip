@@ -221,6 +221,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
     // VALU instructions placed after each MFMA of a k16 sub-step (a scheduling hint: the
     // next step's fragment decode, ~24 (Q4_K) or ~36 (Q6_K) per sub-step)
     constexpr int kValuPerMfma = Q4 ? 2 : 3;
+    // the first sub-step also carries the factors of the next step
+    constexpr int kValuFirst = Q4 ? 4 : 5;
 
     // ---- fragments of step s from its raw bytes: fb[j][kk] covers k 16kk + 8hl + 0..7.
     // Factors first (one set per column and step, Q6_K one per k16 sub-step), then
@@ -325,7 +327,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
     // Pipeline.  x streams three steps ahead through four LDS buffers (step s reads buffer
     // s % 4 = its index within the super-block, a compile-time constant; x(s+3) goes into
     // buffer (s-1) % 4, whose last reads, at step s-1, every wave finished before the
-    // barrier ending step s-1).  Raw weights: Q4_K step s decodes from slot s % 4, refilled
+    // barrier ending step s-1; the barrier ending step s makes x(s+2) visible).  Raw weights: Q4_K step s decodes from slot s % 4, refilled
     // with raw(s+4) at step s; Q6_K step pair u = s/2 uses slot u&1, refilled with pair u+2 at
     // step 2u+1.  The decode of step s+1 runs during the MFMAs of step s, so fragments are
     // double-buffered.
@@ -348,6 +350,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
     __syncthreads();
 
     half8_t fb[2][NJ][4];
+    // A fragments: a[kk & 1] feeds sub-step kk; the kk = 0 fragments of step s+1 are read
+    // during the last sub-step of step s, before the barrier that ends it.
+    half8_t a[2][MI];
+    load_a(0, 0, a[0]);
     {
         Factors F;
         factors(sbeg, raw[0], F);
@@ -371,18 +377,18 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
             dma_x(s + 3, (jstep + 3) & 3);
             if constexpr (Q4) load_raw(s + 4, raw[jstep]);  // slot of step s, decoded during step s-1
             else if (jstep & 1) load_raw(s + 3, raw[(jstep >> 1) & 1]);
-            half8_t a[2][MI];
             // Each k16 sub-step is its own scheduling region: its 16 MFMAs (independent
-            // accumulators), the next sub-step's 8 A reads and one fragment per column of
-            // the next step's decode, issued interleaved so that the LDS and VALU work runs
-            // in the MFMA shadow.  The first A reads and the next step's factors precede.
-            load_a(jstep, 0, a[0]);
+            // accumulators), the next sub-step's 8 A reads (in the last sub-step: the first
+            // ones of step s+1, from buffer (s+1) % 4, whose x every wave waited for before
+            // the barrier that ended step s-1) and one fragment per column of the next
+            // step's decode, issued interleaved so that the LDS and VALU work runs in the
+            // MFMA shadow.  The next step's factors precede.
             Factors F;
             factors(s + 1, raw[rn], F);
-            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
                 if (kk < 3) load_a(jstep, kk + 1, a[(kk + 1) & 1]);
+                else load_a((jstep + 1) & 3, 0, a[0]);
 #pragma unroll
                 for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -393,28 +399,31 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
 #pragma unroll
                 for (int m = 0; m < MI; ++m) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    if (kk < 3) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    if (kk == 0) __builtin_amdgcn_sched_group_barrier(0x002, kValuFirst, 0);
+                    else __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);
+                    if (kk == 0) __builtin_amdgcn_sched_group_barrier(0x002, kValuFirst, 0);
+                    else __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
-            // x(s+1) must be in LDS for every wave: wait for its DMA (issued at step s-2), then
-            // meet at the barrier.  Loads issued after x(s+1), in order: Q4_K raw(s+2) [step s-2],
-            // x(s+2), raw(s+3) [s-1], x(s+3), raw(s+4) [s]; Q6_K the x DMAs of steps s-1 and s
-            // and the raw pairs issued after x at odd steps among s-2, s-1, s: one (s even) or
-            // two (s odd).  The count is exact but for the first steps, whose x the prologue
+            // x(s+2) must be in LDS for every wave (step s+1 reads its first fragments in its
+            // last sub-step): wait for its DMA (issued at step s-1), then meet at the barrier.
+            // Loads issued after x(s+2), in order: Q4_K raw(s+3) [step s-1], x(s+3), raw(s+4)
+            // [s]; Q6_K the x DMA of step s and the raw pair issued after x at the odd one of
+            // steps s-1, s.  The count is exact but for the first step, whose x the prologue
             // already waited for (a count above the loads in flight then waits for nothing
-            // that matters).
+            // that matters).  The barrier also orders every wave's reads of buffer s % 4
+            // (the fragments of step s, all consumed by its MFMAs) before step s+1's DMA of
+            // x(s+4) into that buffer.
             // The barrier is the bare s_barrier: __syncthreads() adds a workgroup fence, which
             // the compiler implements by waiting for every LDS DMA in flight (x(s+2), x(s+3)
             // too).  The explicit wait above covers what the other waves read next, and the
             // signal fences keep the compiler from moving memory accesses across the barrier.
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (Q4) vm_wait<3 * kRawLoads + 2 * XDMA>();
-            else if (jstep & 1) vm_wait<2 * kRawLoads + 2 * XDMA>();
-            else vm_wait<kRawLoads + 2 * XDMA>();
+            if constexpr (Q4) vm_wait<2 * kRawLoads + XDMA>();
+            else vm_wait<kRawLoads + XDMA>();
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __builtin_amdgcn_s_barrier();
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
