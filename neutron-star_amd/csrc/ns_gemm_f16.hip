@@ -111,7 +111,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
     auto xbuf = [&](int buf) -> u32x4 * { return buf == 0 ? Xs0 : buf == 1 ? Xs1 : buf == 2 ? Xs2 : Xs3; };
     __shared__ uint32_t last_flag, late_flag;
 
-    const uint32_t tid = threadIdx.x, lane = tid & 63, hl = lane >> 5;
+    uint32_t tid = threadIdx.x, lane = tid & 63, hl = lane >> 5;  // formed again after the main loop
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // XCD-aware order: workgroup L runs on XCD L % 8; work item q = (kp * ntok + tt) * ncol + ct,
     // and XCD x takes the contiguous run [x*W/8, (x+1)*W/8), so its L2 holds whole x slices.
@@ -430,6 +430,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
         }
     }
     vm_wait<0>();  // the refills issued past the last step have landed
+    // Past the main loop the lane values and 1/c_r = 2^24 / (c_r 2^24) (exact: powers of two)
+    // are formed again rather than kept live across it, where every VGPR is taken and they
+    // would go to scratch.  The lane index comes from a volatile asm so that the compiler
+    // cannot hoist it above the loop.
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+    hl = lane >> 5;
+    tid = wave * 64 + lane;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+        inv_c[j] = __builtin_bit_cast(float, (uint32_t(2 * 127 + 24) << 23) - __builtin_bit_cast(uint32_t, c24[j]));
 
     // ---- outputs.  32x32 D layout: lane holds column lane%32 and rows
     // 8*(v/4) + 4*(lane/32) + v%4 for v = 0..15.
