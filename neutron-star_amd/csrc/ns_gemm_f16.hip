@@ -186,10 +186,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
         voff[j] = uint32_t(region_offset(TYPE, r / kRowTile, 0, nb)) + (r % kRowTile) * 16;
     }
     constexpr uint32_t kRegion = kRowTile * block_bytes(TYPE);  // bytes of one (slab, super-block) region
-    auto load_raw = [&](uint32_t s, Raw (&raw)[NJ]) {
+    // Column jc's raw bytes of step s (jc < 0: every column).
+    auto load_raw = [&](uint32_t s, Raw (&raw)[NJ], int jc = -1) {
         const uint32_t b = s >> 2;
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
+            if (jc >= 0 && j != jc) continue;
             if constexpr (Q4) {
                 const uint32_t p = s & 3;
                 raw[j].qa = __builtin_amdgcn_raw_buffer_load_b64(wsrc(j), int(voff[j] + 8 * hl), int(b * kRegion + (1 + 2 * p) * 1024), 0);
@@ -299,9 +301,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
         const uint32_t R = 8 * (wave + kWaves * uint32_t(i)) + (lane >> 3), c = (lane & 7) ^ ((R >> 1) & 7);
         xoff[i] = ((t0 + R) * cols + 8 * c) * 2;
     }
-    auto dma_x = [&](uint32_t s, int buf) {
+    auto dma_x = [&](uint32_t s, int buf, int i0 = 0, int i1 = XDMA) {  // instructions i0 .. i1-1
 #pragma unroll
         for (int i = 0; i < XDMA; ++i) {
+            if (i < i0 || i >= i1) continue;
             const uint32_t rbase = 8 * (wave + kWaves * uint32_t(i));
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 xsrc, (__attribute__((address_space(3))) void *)(xbuf(buf) + rbase * 8), 16, xoff[i], s * KS * 2, 0, 0);
@@ -327,12 +330,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
     // Pipeline.  x streams three steps ahead through four LDS buffers (step s reads buffer
     // s % 4 = its index within the super-block, a compile-time constant; x(s+3) goes into
     // buffer (s-1) % 4, whose last reads, at step s-1, every wave finished before the
-    // barrier ending step s-1; the barrier ending step s makes x(s+2) visible).  Raw weights: Q4_K step s decodes from slot s % 4, refilled
-    // with raw(s+4) at step s; Q6_K step pair u = s/2 uses slot u&1, refilled with pair u+2 at
-    // step 2u+1.  The decode of step s+1 runs during the MFMAs of step s, so fragments are
-    // double-buffered.
-    // Q4_K raw weights stream four steps ahead through four slots (step s decodes from slot
-    // s % 4, its index in the super-block), Q6_K one step pair ahead through two pair slots.
+    // barrier ending step s-1; the barrier ending step s makes x(s+2) visible).  Raw weights:
+    // Q4_K step s decodes from slot s % 4, refilled with raw(s+4) during step s; Q6_K step
+    // pair u = s/2 uses slot u&1, refilled with pair u+2 during step 2u+1.  A refill has
+    // landed by the end of the step after the one that issued it.  The decode of step s+1
+    // runs during the MFMAs of step s, so fragments are double-buffered.
     constexpr int kSlots = Q4 ? 4 : 2;
     Raw raw[kSlots][NJ];
     const uint32_t sbeg = 4 * sb0, send = 4 * sb1;
@@ -374,9 +376,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
             // such loads read in-bounds or descriptor-clamped bytes (zeros) into registers and
             // into an x buffer no wave reads again, and a branch around them would make the
             // compiler wait for every load at the merge.
-            dma_x(s + 3, (jstep + 3) & 3);
-            if constexpr (Q4) load_raw(s + 4, raw[jstep]);  // slot of step s, decoded during step s-1
-            else if (jstep & 1) load_raw(s + 3, raw[(jstep >> 1) & 1]);
             // Each k16 sub-step is its own scheduling region: its 16 MFMAs (independent
             // accumulators), the next sub-step's 8 A reads (in the last sub-step: the first
             // ones of step s+1, from buffer (s+1) % 4, whose x every wave waited for before
@@ -387,6 +386,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
             factors(s + 1, raw[rn], F);
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
+                // The step's global loads, spread over its four sub-steps: x(s+3) into buffer
+                // (s-1) % 4, two instructions per sub-step, and the raw refill, one column per
+                // sub-step (Q4_K: slot s % 4, decoded during step s-1; Q6_K at odd steps: the
+                // pair slot of steps s-1 and s).  Issued as one burst after the barrier, the
+                // four waves' loads stalled the matrix pipe for ~15% of every step.
+                static_assert(XDMA == 8, "two x instructions per sub-step");
+                dma_x(s + 3, (jstep + 3) & 3, 2 * kk, 2 * kk + 2);
+                if (kk < NJ) {
+                    if constexpr (Q4) load_raw(s + 4, raw[jstep], kk);
+                    else if (jstep & 1) load_raw(s + 3, raw[(jstep >> 1) & 1], kk);
+                }
                 if (kk < 3) load_a(jstep, kk + 1, a[(kk + 1) & 1]);
                 else load_a((jstep + 1) & 3, 0, a[0]);
 #pragma unroll
@@ -410,20 +420,20 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
             }
             // x(s+2) must be in LDS for every wave (step s+1 reads its first fragments in its
             // last sub-step): wait for its DMA (issued at step s-1), then meet at the barrier.
-            // Loads issued after x(s+2), in order: Q4_K raw(s+3) [step s-1], x(s+3), raw(s+4)
-            // [s]; Q6_K the x DMA of step s and the raw pair issued after x at the odd one of
-            // steps s-1, s.  The count is exact but for the first step, whose x the prologue
-            // already waited for (a count above the loads in flight then waits for nothing
-            // that matters).  The barrier also orders every wave's reads of buffer s % 4
-            // (the fragments of step s, all consumed by its MFMAs) before step s+1's DMA of
-            // x(s+4) into that buffer.
+            // The wait leaves in flight exactly the loads issued during step s (x(s+3), and the
+            // raw refill: Q4_K every step, Q6_K at odd steps), so it does not depend on the
+            // order in which the compiler schedules them within the step; everything issued
+            // at step s-1, x(s+2) included, has landed.  The barrier also orders every wave's
+            // reads of buffer s % 4 (the fragments of step s, all consumed by its MFMAs) before
+            // step s+1's DMA of x(s+4) into that buffer.
             // The barrier is the bare s_barrier: __syncthreads() adds a workgroup fence, which
             // the compiler implements by waiting for every LDS DMA in flight (x(s+2), x(s+3)
             // too).  The explicit wait above covers what the other waves read next, and the
             // signal fences keep the compiler from moving memory accesses across the barrier.
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (Q4) vm_wait<2 * kRawLoads + XDMA>();
-            else vm_wait<kRawLoads + XDMA>();
+            if constexpr (Q4) vm_wait<kRawLoads + XDMA>();
+            else if (jstep & 1) vm_wait<kRawLoads + XDMA>();
+            else vm_wait<XDMA>();
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __builtin_amdgcn_s_barrier();
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
