@@ -9,8 +9,9 @@
 // Integer-exact tiles.  Inside one 256-wide super-block every weight is
 //   Q4_K: w = d * (sc_g * q) - dmin * m_g      (quant.cpp:11)
 //   Q6_K: w = d * (sc_s * (v - 32))            (quant.cpp:17)
-// where sc*q (<= 945) and sc*(v-32) (|.| <= 1024) are integers that fp16
-// represents exactly.  The LDS weight tile therefore holds those integers, the
+// where sc*q (<= 945) and sc*(v-32) are integers that fp16 represents exactly
+// (Q6_K: while |sc| <= 64; the int8 scales of real tensors can need one more bit,
+// and those tile values are rounded once, see decode(RawQ6)).  The LDS weight tile therefore holds those integers, the
 // MFMA products with fp16 x are exact, and the per-row factors are applied once
 // per super-block on the accumulators:
 //   Y += d * acc_sb  [- dmin * sum_g m_g * S_g(x)]            (S_g = sum of x over group g)
@@ -199,21 +200,28 @@ __device__ __forceinline__ void load_raw(rsrc_t w, uint32_t row, uint32_t nb, ui
     }
 }
 
-// Values: sc * (v - 32), sc = scales[8h + 2qa + l/16], exact in fp16.
+// Values: sc * (v - 32), sc = scales[8h + 2qa + l/16]: v - 32 exactly (one packed add to the
+// fp16 1024 + v), then one rounding of the product.  The product is exact while it fits 11
+// significant bits (always for |sc| <= 64, the synthetic generator's -32..31 included); real
+// int8 scales (llama.cpp puts one group of every Q6_K block at -128) reach |sc*(v-32)| = 4096,
+// where odd products need 12 bits and round (relative error <= 2^-12 on those weights).  The
+// single FMA sc*(1024+v) - 1056*sc would need the bias 1056*sc, which is not an fp16 past
+// |sc| = 62.
 __device__ __forceinline__ void decode(const RawQ6 &r, uint32_t s, uint32_t hh, float z, WRun &out) {
     const uint32_t sr = s & 3, h = sr >> 1, qa = 2 * (sr & 1) + hh;
     const uint32_t si = 8 * h + 2 * qa;
     const uint32_t nshift = qa >= 2 ? 4 : 0, hshift = 2 * qa;
+    const half2_t m1056 = {_Float16(-1056.f), _Float16(-1056.f)};
+    auto scaled = [&](half2_t t, half2_t sc2) { return u32((t + m1056) * sc2); };
 #pragma unroll
     for (int c = 0; c < 2; ++c) {  // l = 16c .. 16c+15
         const _Float16 s16 = _Float16(z * float(int8_t(byte_of(r.scw[(si + c) >> 2], int((si + c) & 3)))));
         const half2_t sc2 = {s16, s16};
-        const half2_t nb2 = {_Float16(-1056.f) * s16, _Float16(-1056.f) * s16};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {  // l = 16c + 4i .. +3
             const uint32_t v = ((r.ql[c][i] >> nshift) & 0x0F0F0F0Fu) | (((r.qh[c][i] >> hshift) & 0x03030303u) << 4);
-            out.v[2 * c + (i >> 1)][(i & 1) * 2 + 0] = scale_pair(magic_pair(v, kSel01, kMask6), sc2, nb2);
-            out.v[2 * c + (i >> 1)][(i & 1) * 2 + 1] = scale_pair(magic_pair(v, kSel23, kMask6), sc2, nb2);
+            out.v[2 * c + (i >> 1)][(i & 1) * 2 + 0] = scaled(magic_pair(v, kSel01, kMask6), sc2);
+            out.v[2 * c + (i >> 1)][(i & 1) * 2 + 1] = scaled(magic_pair(v, kSel23, kMask6), sc2);
         }
     }
 }
@@ -378,7 +386,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
             }
         }
         float inv_c;
-        row_scale(M, c24, inv_c);
+        row_scale(M, c24, inv_c, TYPE == Q6_K);
         if (hh == 0) colInv[wc] = inv_c;
     }
 

@@ -172,7 +172,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             M[j] = __builtin_fmaxf(M[j], __shfl_xor(M[j], 32));
-            row_scale(M[j], c24[j], inv_c[j]);
+            row_scale(M[j], c24[j], inv_c[j], !Q4);
         }
     }
 

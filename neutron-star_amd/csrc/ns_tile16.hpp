@@ -10,8 +10,12 @@
 // tile is formed by one packed fp16 FMA straight from the quant bits:
 //
 //   M_r  = max over the row's super-blocks of max(|d|, |dmin|)  (Q6_K: |d|)
-//   c_r  = 2^(-15 - ceil(log2 M_r))      (c_r = 1 when M_r = 0)
-//   A    = RNE16(d * sc * 2^24 * c_r)    (<= 63 * 2^9: always an fp16 normal or subnormal)
+//   c_r  = 2^(-15 - E_r), E_r = ceil(log2 M_r)  (Q6_K: E_r = floor(log2 M_r) + 1, the
+//          power of two strictly above M_r; c_r = 1 when M_r = 0)
+//   A    = RNE16(d * sc * 2^24 * c_r)    (Q4_K: |A| <= 63 * 2^9; Q6_K, int8 sc down to -128:
+//          |A| <= 2^16 * M_r / 2^E_r <= 65504, the fp16 maximum.  With ceil, a row whose
+//          largest d is a power of two and whose block has sc = -128, as llama.cpp's
+//          quantiser gives every Q6_K block, would put A at -2^16, past fp16's range)
 //   B    = RNE16(-dmin * m * c_r)        (Q6_K: RNE16(-32 * d * sc * c_r))
 //   F    = RNE16(q * 2^-24 * A + B)      (one rounding: the packed FMA is fused)
 //
@@ -32,10 +36,11 @@
 namespace ns {
 
 // Row scale: returns c * 2^24 (the A factor's scale) and 1/c (the output's).
-// M is the largest |factor| of the row in fp32 (every fp16 is an fp32 normal).
-__device__ __forceinline__ void row_scale(float M, float &c24, float &inv_c) {
+// M is the largest |factor| of the row in fp32 (every fp16 is an fp32 normal);
+// above (Q6_K rows) takes the power of two strictly above M instead of ceil(log2 M).
+__device__ __forceinline__ void row_scale(float M, float &c24, float &inv_c, bool above) {
     const uint32_t b = __builtin_bit_cast(uint32_t, M);
-    const int e = int(b >> 23) - 127 + ((b & 0x7FFFFFu) != 0u);  // ceil(log2 M)
+    const int e = int(b >> 23) - 127 + ((above || (b & 0x7FFFFFu) != 0u) ? 1 : 0);  // E_r
     const bool pos = M > 0.f;
     c24 = pos ? __builtin_bit_cast(float, uint32_t(127 + 9 - e) << 23) : 16777216.0f;
     inv_c = pos ? __builtin_bit_cast(float, uint32_t(127 + 15 + e) << 23) : 1.0f;

@@ -131,7 +131,8 @@ static int check(int type, int layout, uint64_t cols, uint64_t rows) {
  * with a per-row power of two c folded in so that the tile is one packed fp16 FMA
  * from the quant bits (this build's kernels, neutron-star_amd/csrc/ns_tile16.hpp):
  *   M = max over the row's blocks of max(|d|, |dmin|) (Q6_K: |d|)
- *   c = 2^(-15 - ceil(log2 M)), c = 1 when M == 0
+ *   c = 2^(-15 - E), E = ceil(log2 M) (Q6_K: floor(log2 M) + 1, the power of two strictly
+ *       above M, so that A = d*sc*2^24*c stays within fp16 for sc = -128), c = 1 when M == 0
  *   A = RNE16(d*sc*2^24*c),  B = RNE16(-dmin*m*c)  (Q6_K: B = RNE16(-32*d*sc*c))
  *   F = RNE16(q*2^-24*A + B)                       (Q6_K: q is the 6-bit v)
  * and the output is RNE11((sum_k F*x) / c).  Every quantity before RNE16 is exact
@@ -175,7 +176,8 @@ static void row_scale(int type, int layout, const uint8_t *w, uint64_t cols, uin
     }
     int ex;
     const double m = frexp(M, &ex);      /* M = m * 2^ex */
-    const int e = m == 0.5 ? ex - 1 : ex; /* ceil(log2 M) */
+    /* ceil(log2 M); Q6_K: floor(log2 M) + 1 = ex */
+    const int e = (m == 0.5 && type == NSO_Q4_K) ? ex - 1 : ex;
     *c24 = ldexp(1.0, 9 - e);
     *inv_c = ldexp(1.0, 15 + e);
 }

@@ -339,6 +339,33 @@ def test_f16_tile_known_roundings():
     assert iz[0] == 1.0 and not np.any(tz)
 
 
+def test_f16_tile_q6k_row_scale_and_int8_extremes():
+    """Q6_K rows take the power of two strictly above M: M = 2 gives E = 2, c = 2^-17 (a Q4_K row
+    with M = 2 takes E = 1).  Hand-computed tiles for d = 2 and sc = -128, the scale llama.cpp's
+    quantiser gives the largest group of every Q6_K block: A = RNE16(2 * -128 * 2^24 * 2^-17) =
+    -2^15 (with E = 1 it would be -2^16, past fp16's range), B = RNE16(-32 * 2 * -128 * 2^-17) =
+    2^-4; v = 0 gives B, v = 63 gives 63 * 2^-24 * -2^15 + 2^-4 = -31 * 2^-9 (exact), and F/c
+    are the weights 8192 and -7936.  sc = 127 with v = 63: c*w = 2 * 127 * 31 * 2^-17 is 1968.5
+    ulps of 2^-15, a tie that RNE16 takes to 1968: F/c = 7872 (the FP16 mode's one rounding)."""
+    sc = np.full(16, 127)
+    sc[0] = -128
+    v = np.zeros(256, dtype=np.int64)
+    v[1] = 63
+    v[16] = 63  # group 1 (sc = 127)
+    w = q6k_block(np.float16(2.0), sc, v)
+    tile, inv = O.f16_tile_rows(O.Q6_K, O.ROW_MAJOR, w, 256, 1)
+    assert inv[0] == 2.0 ** 17
+    assert tile[0, 0] == np.float32(2.0 ** -4)
+    assert tile[0, 1] == np.float32(-31 * 2.0 ** -9)
+    assert tile[0, 0] * inv[0] == 8192.0 and tile[0, 1] * inv[0] == -7936.0
+    assert tile[0, 16] == np.float32(1968 * 2.0 ** -15) and tile[0, 16] * inv[0] == 7872.0
+    assert np.isfinite(tile).all()
+    # away from powers of two the row scale is ceil(log2 M), as for Q4_K
+    for dv, expect in ((2.0 + 2.0 ** -9, 2.0 ** 17), (1.5, 2.0 ** 16), (2.0 ** -24, 2.0 ** -8)):
+        _, inv6 = O.f16_tile_rows(O.Q6_K, O.ROW_MAJOR, q6k_block(np.float16(dv), sc, v), 256, 1)
+        assert inv6[0] == np.float32(expect), (dv, inv6[0])
+
+
 def test_f16_tile_error_bound():
     """On BASELINE-distributed blocks, F/c differs from the exact weight w by at most the three
     roundings of A, B and F: |F/c - w| <= 2^-11 * (|d*sc*q| + |dmin*m| + |w|) * (1 + 2^-10)
