@@ -6,7 +6,8 @@ super-block as llama.cpp quantises it puts its largest group at a scale near
 reads Q6_K weights is run here on blocks whose scales span -128..127 (each
 block has one group at -128 or 127, and six-bit values at 0 and 63), against
 the oracle: the prefill GEMM in both accumulation modes and every layout, the
-decode GEMV, the one-launch decode block and batch 2-4.  Bars as elsewhere:
+decode GEMV, the one-launch decode block, batch 2-4, the dequantisation check
+hook and the embedding (bit-exact).  Bars as elsewhere:
 FP32 mode 1e-3, FP16 mode 1e-2 against the FP32 oracle and 1e-3 against the
 FP16-mode oracle.
 """
@@ -75,8 +76,9 @@ def test_prefill_down_full_range_scales(ctx, layout, fast):
 
 
 def test_prefill_down_full_range_scales_power_of_two_d(ctx):
-    """The FP16 mode's row scale makes d*c_r exactly 2^-15 when a row's largest d is a power of
-    two; with sc = -128 the tile factor A = d*sc*2^24*c_r is then -2^16, one past fp16's range."""
+    """A row whose largest d is a power of two, with sc = -128: a row scale of 2^-(15 + ceil(log2 M))
+    would make d*c_r exactly 2^-15 and the FP16-mode tile factor A = d*sc*2^24*c_r = -2^16, one
+    past fp16's range; the Q6_K row scale takes the power of two strictly above M instead."""
     cols, rows, batch = 1024, 128, 64
     host = full_range_q6k(0x7C, rows, cols)
     blk = host.reshape(-1, 210).copy()
@@ -142,3 +144,25 @@ def test_decode_block_full_range_scales(ctx):
     href = O.gate_up_geglu(O.ROW_MAJOR, g, u, D, F, x)
     yref = O.gemv(N.Q6_K, O.ROW_MAJOR, dn, F, D, href.astype(np.float32))
     assert rel_err(y.cpu().numpy(), yref) <= 1e-3
+
+
+@pytest.mark.parametrize("layout", [N.CDNA4, N.NSMFFN, N.ROW_MAJOR], ids=LNAME.get)
+def test_dequant_and_embedding_full_range_scales(ctx, layout):
+    """The check hook and the token embedding stay bit-exact at int8 scales -128..127."""
+    cols, rows = 1024, 128
+    host = full_range_q6k(0x86, rows, cols)
+    w = on_device(host, cols, rows, layout)
+    out32 = torch.empty((rows, cols), dtype=torch.float32, device="cuda")
+    out16 = torch.empty((rows, cols), dtype=torch.int16, device="cuda")
+    ctx.dequant(w, N.Q6_K, layout, cols, rows, 0, rows, out32, out16)
+    ids = np.array([0, rows - 1, 77, 77], dtype=np.int32)
+    scale = np.float32(np.sqrt(3840.0))
+    emb = torch.empty((len(ids), cols), dtype=torch.float32, device="cuda")
+    ctx.embedding(w, N.Q6_K, layout, cols, rows, torch.from_numpy(ids).cuda(), len(ids), float(scale), emb)
+    torch.cuda.synchronize()
+    want = O.dequant_rows(N.Q6_K, O.ROW_MAJOR, host, cols, rows)
+    assert np.array_equal(out32.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(out16.cpu().numpy().view(np.uint16), want.astype(np.float16).view(np.uint16))
+    got = emb.cpu().numpy()
+    for t, r in enumerate(ids):
+        np.testing.assert_array_equal(got[t].view(np.uint32), (scale * want[r]).astype(np.float32).view(np.uint32))
