@@ -35,7 +35,9 @@ def ctx():
 
 def full_range_q6k(seed, rows, cols, d_lo=1e-4, d_hi=2e-3):
     """Row-major Q6_K blocks: scales uniform in -128..127 with one group of each block at
-    -128 or 127, six-bit values uniform with runs at 63 and 0, d uniform in [d_lo, d_hi]."""
+    -128 or 127, six-bit values uniform with runs at 63 and 0, |d| uniform in [d_lo, d_hi] with
+    either sign (llama.cpp's Q6_K quantiser stores d = 1/iscale with iscale = -128/max, so d is
+    usually negative)."""
     rng = np.random.default_rng(seed)
     nb = rows * cols // 256
     blocks = []
@@ -45,7 +47,8 @@ def full_range_q6k(seed, rows, cols, d_lo=1e-4, d_hi=2e-3):
         v = rng.integers(0, 64, 256)
         v[(i % 8) * 32:(i % 8) * 32 + 8] = 63
         v[(i % 8) * 32 + 8:(i % 8) * 32 + 16] = 0
-        blocks.append(q6k_block(np.float16(rng.uniform(d_lo, d_hi)), sc, v))
+        d = rng.uniform(d_lo, d_hi) * (-1.0 if rng.random() < 0.75 else 1.0)
+        blocks.append(q6k_block(np.float16(d), sc, v))
     return np.concatenate(blocks)
 
 
