@@ -288,7 +288,12 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
             }
             // x(s+1) must be in LDS for every wave: wait for its DMA (issued one step
             // ago; the loads issued after it -- raw(s+1), x(s+2), raw(s+2) -- may stay
-            // in flight), then meet at the barrier.
+            // in flight), then meet at the barrier.  The barrier is the bare s_barrier:
+            // __syncthreads() adds a workgroup fence, which the compiler implements by also
+            // waiting for x(s+2)'s DMA, issued this step.  The barrier orders every wave's
+            // reads of buffer s % 3 (all consumed by this step's MFMAs) before the DMA of
+            // x(s+3) into it; the signal fences keep the compiler from moving memory
+            // accesses across it.
             __builtin_amdgcn_sched_barrier(0);
             if (s + 2 < send) {
                 constexpr int n = kRawLoads + XDMA + kRawLoads;
@@ -296,7 +301,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
             } else {
                 __builtin_amdgcn_s_waitcnt(0);
             }
-            __syncthreads();
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_s_barrier();
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
         }
     }
 
