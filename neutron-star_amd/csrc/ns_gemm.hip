@@ -19,7 +19,9 @@
 // groups: A = the group sums of x split into fp16 hi + lo (k 0..7 and 8..15),
 // B = the min factors, likewise as fp16 hi + lo.  This keeps the FP32 mode at fp32 accuracy (a plain fp16 copy of the
 // dequantised weights would add ~1e-3 relative error by itself) and needs fewer
-// VALU operations per weight than materialising d*sc*q - dmin*m.
+// VALU operations per weight than materialising d*sc*q - dmin*m.  A token whose group
+// sums pass fp16's range enters as x * 2^-k (group_sums_kernel, copy_scaled_kernel) and
+// its outputs are multiplied by 2^k after the loop.
 //
 // Tiling: one workgroup (256 threads = 4 wave64) computes 128 tokens x 128
 // columns with v_mfma_f32_32x32x16_f16; columns are 128 weight rows (plain) or
@@ -54,6 +56,7 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
 constexpr int TT = 256;        // tokens per workgroup tile
+static_assert(256 % TT == 0, "a token tile lies inside one 256-token block of the rescaled copy");
 constexpr int TC = 256;        // B columns per workgroup tile
 constexpr int kWaves = 8;      // 2 (tokens) x 4 (columns)
 constexpr int kThreads = 64 * kWaves;
@@ -337,10 +340,18 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     // PAIR: gate columns 0..127 come from waves with (wave & 3) < 2: wave-uniform
     const rsrc_t wsrc = make_rsrc((PAIR && (wave & 3) >= 2) ? w1 : w0, wbytes);
     const uint32_t wrow = r0 + (PAIR ? (wc % (TC / 2)) : wc);
-    const rsrc_t xsrc = make_rsrc(x, batch * cols * 2);
     // x group sums: plane hi [batch][ngroups] then plane lo; rows past batch are
     // never stored, so their (lo-plane) contents do not matter
     const rsrc_t xssrc = make_rsrc(xsums, (Q4 && !F16) ? 2 * batch * ngroups * 2 : 0);
+    // Q4_K FP32 mode: a tile in a 256-token block with a rescaled token reads x from the
+    // rescaled copy, which holds every row of that block, and multiplies its tokens'
+    // outputs back by their factor (TT divides 256)
+    const float *xsb = reinterpret_cast<const float *>(xsums);
+    const XsLayout xl = xs_layout(cols, batch);
+    uint32_t tile_scaled = 0;  // one uniform load
+    if constexpr (Q4 && !F16)
+        tile_scaled = __builtin_amdgcn_readfirstlane(reinterpret_cast<const uint32_t *>(xsb + xl.bflag)[t0 / 256]);
+    const rsrc_t xsrc = make_rsrc(tile_scaled ? static_cast<const void *>(xsb + xl.xcopy) : x, batch * cols * 2);
 
     float16_t acc[MI][NJ];
 #pragma unroll
@@ -552,6 +563,18 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     auto tok_of = [&](int i, int v) -> uint32_t {
         return t0 + wt * WT + uint32_t(i) * 32 + 8 * uint32_t(v >> 2) + 4 * (lane >> 5) + uint32_t(v & 3);
     };
+    // rescaled tokens: times 2^k_t, exact in fp32, so also before the split-K parts are added
+    if (tile_scaled) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const uint32_t t = tok_of(i, v);
+                const float tf = t < batch ? xsb[xl.tfac + t] : 1.f;
+#pragma unroll
+                for (int jj = 0; jj < NJ; ++jj) acc[i][jj][v] *= tf;
+            }
+    }
     auto col_row = [&](int jj) -> uint32_t {  // weight row of B fragment jj
         if constexpr (PAIR) return r0 + wn * 32 + (lane & 31);
         else return r0 + bcol(jj) + (lane & 31);
@@ -765,25 +788,85 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     }
 }
 
-// Group sums of x for the Q4_K min term: s = sum of 32 fp16 values in fp32,
-// stored as hi = fp16(s) and lo = fp16(s - hi) (together ~22 significant bits).
-__global__ void group_sums_kernel(const uint16_t *__restrict__ x, uint32_t cols, uint32_t batch,
-                                  uint16_t *__restrict__ hi, uint16_t *__restrict__ lo) {
-    const uint32_t ng = cols / 32;
-    const uint64_t idx = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (idx >= uint64_t(batch) * ng) return;
-    const uint32_t t = uint32_t(idx / ng), g = uint32_t(idx % ng);
-    const half8_t *p = reinterpret_cast<const half8_t *>(x + size_t(t) * cols + size_t(g) * 32);
-    float s = 0.f;
+// Group sums of x for the Q4_K min term (the XsLayout block): one workgroup per 8
+// tokens, one wave per token.  s = sum of 32 fp16 values in fp32, stored as
+// hi = fp16(s) and lo = fp16(s - hi) (together ~22 significant bits).  A token whose
+// largest |s| exceeds 65504 (fp16's largest finite value) gets the smallest k_t with
+// max |s| * 2^-k_t <= 65504, and its sums are taken again over fp16(x * 2^-k_t), the
+// values copy_scaled_kernel writes for it, so the GEMM's x tile and its min term see
+// the same operands.  Finite x needs k_t <= 6.
+__global__ __launch_bounds__(512) void group_sums_kernel(const uint16_t *__restrict__ x, uint32_t cols,
+                                                         uint32_t batch, float *__restrict__ xs) {
+    __shared__ uint32_t kshift[8];
+    const XsLayout L = xs_layout(cols, batch);
+    const uint32_t ng = cols / 32, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t t = blockIdx.x * 8 + w;
+    const bool live = t < batch;
+    uint16_t *hi = reinterpret_cast<uint16_t *>(xs + L.sums), *lo = hi + size_t(batch) * ng;
+    const uint16_t *row = x + size_t(t) * cols;
+    auto sum32 = [&](uint32_t g, _Float16 f) {
+        const half8_t *p = reinterpret_cast<const half8_t *>(row + size_t(g) * 32);
+        float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const half8_t v = p[i];
+        for (int i = 0; i < 4; ++i) {
+            const half8_t v = p[i] * f;  // f = 2^-k: exact but for fp16 subnormal results
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s += float(v[e]);
+            for (int e = 0; e < 8; ++e) s += float(v[e]);
+        }
+        return s;
+    };
+    auto put = [&](uint32_t g, float s) {
+        const _Float16 h = _Float16(s);
+        hi[size_t(t) * ng + g] = __builtin_bit_cast(uint16_t, h);
+        lo[size_t(t) * ng + g] = __builtin_bit_cast(uint16_t, _Float16(s - float(h)));
+    };
+    float mx = 0.f;
+    if (live)
+        for (uint32_t g = lane; g < ng; g += 64) {
+            const float s = sum32(g, _Float16(1.0f));
+            put(g, s);
+            mx = __builtin_fmaxf(mx, __builtin_fabsf(s));
+        }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, o));
+    uint32_t k = 0;
+    while (mx > 65504.f && k < 6) {  // finite x: |s| <= 32 * 65504 < 65504 * 2^5
+        mx *= 0.5f;
+        ++k;
     }
-    const _Float16 h = _Float16(s);
-    hi[idx] = __builtin_bit_cast(uint16_t, h);
-    lo[idx] = __builtin_bit_cast(uint16_t, _Float16(s - float(h)));
+    if (lane == 0) kshift[w] = k;
+    __syncthreads();
+    uint32_t any = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) any |= kshift[i];
+    if (threadIdx.x == 0) reinterpret_cast<uint32_t *>(xs + L.gflag)[blockIdx.x] = any != 0;
+    if (!live) return;
+    if (lane == 0) xs[L.tfac + t] = float(1u << k);
+    if (k != 0) {
+        const _Float16 f = _Float16(1.0f / float(1u << k));
+        for (uint32_t g = lane; g < ng; g += 64) put(g, sum32(g, f));
+    }
+}
+
+// The rescaled copy of x: every token of a 256-token block (the GEMM token tiles lie
+// inside such blocks) with any flagged 8-row group is copied as fp16(x * 2^-k_t), so a
+// GEMM tile with a rescaled token reads all its rows from xcopy; the block's flag goes to
+// bflag, the one word a GEMM workgroup reads.  One workgroup per 8 tokens; blocks without
+// a flag return at once.
+__global__ __launch_bounds__(512) void copy_scaled_kernel(const uint16_t *__restrict__ x, uint32_t cols,
+                                                          uint32_t batch, float *__restrict__ xs) {
+    const XsLayout L = xs_layout(cols, batch);
+    const uint32_t *gflag = reinterpret_cast<const uint32_t *>(xs + L.gflag);
+    const uint32_t ng8 = (batch + 7) / 8, b0 = blockIdx.x / 32 * 32;
+    const uint32_t t = blockIdx.x * 8 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const uint32_t gi = b0 + (lane & 31);  // lanes 32-63 repeat lanes 0-31
+    const bool any = __ballot(gi < ng8 && gflag[gi] != 0) != 0;
+    if (blockIdx.x % 32 == 0 && threadIdx.x == 0) reinterpret_cast<uint32_t *>(xs + L.bflag)[blockIdx.x / 32] = any;
+    if (!any || t >= batch) return;
+    const _Float16 f = _Float16(1.0f / xs[L.tfac + t]);
+    const half8_t *src = reinterpret_cast<const half8_t *>(x + size_t(t) * cols);
+    half8_t *dst = reinterpret_cast<half8_t *>(reinterpret_cast<uint16_t *>(xs + L.xcopy) + size_t(t) * cols);
+    for (uint32_t c = lane; c < cols / 8; c += 64) dst[c] = src[c] * f;
 }
 
 struct GemmPlan {
@@ -866,11 +949,11 @@ hipError_t launch_layout(int layout, int acc, const uint8_t *w, const uint8_t *u
 
 }  // namespace
 
-// Workspace layout: [Q4_K group sums of x: 2 fp16 planes of batch x cols/32,
-// counted in floats and rounded up to 64] [split-K parts: kparts x planes x tokens x rows,
-// both padded to whole tiles].
+// Workspace layout: [Q4_K: the XsLayout block (group sums of x, token factors, the
+// rescaled copy of x)] [split-K parts: kparts x planes x tokens x rows, both padded to
+// whole tiles].
 static size_t xs_floats(int type, uint32_t cols, uint32_t batch) {
-    return type == Q4_K ? ((size_t(batch) * (cols / 32) + 63) / 64) * 64 : 0;
+    return type == Q4_K ? xs_layout(cols, batch).total : 0;
 }
 
 static void gemm_fp32_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, uint32_t batch, bool pair,
@@ -912,12 +995,12 @@ hipError_t launch_gemm(int type, int layout, int acc, const uint8_t *w, const ui
                        hipStream_t stream) {
     if (layout == CDNA4 && acc == ACC_FP16)
         return launch_gemm_f16(type, w, up, x, out, cols, rows, batch, ws.partial, ws.counters, ws.tune, stream);
-    uint16_t *xh = nullptr, *xl = nullptr;
+    uint16_t *xh = nullptr;
     if (type == Q4_K && acc == ACC_FP32) {  // the exact tiles' min term needs the group sums of x
-        const size_t n = size_t(batch) * (cols / 32);
         xh = reinterpret_cast<uint16_t *>(ws.partial);
-        xl = xh + n;
-        group_sums_kernel<<<dim3(uint32_t((n + 255) / 256)), dim3(256), 0, stream>>>(x, cols, batch, xh, xl);
+        group_sums_kernel<<<dim3((batch + 7) / 8), dim3(512), 0, stream>>>(x, cols, batch, ws.partial);
+        if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+        copy_scaled_kernel<<<dim3((batch + 7) / 8), dim3(512), 0, stream>>>(x, cols, batch, ws.partial);
         if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     }
     const size_t off = xs_floats(type, cols, batch);

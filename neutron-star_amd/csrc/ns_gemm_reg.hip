@@ -48,6 +48,7 @@ typedef __amdgpu_buffer_rsrc_t rsrc_t;
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int TT = 128;              // tokens per workgroup (= per wave)
+static_assert(256 % TT == 0, "a token tile lies inside one 256-token block of the rescaled copy");
 constexpr int MI = TT / 32;          // 32-token MFMA tiles per wave
 constexpr int NJ = 2;                // 32-column MFMA tiles per wave
 constexpr int TC = kWaves * NJ * 32; // B columns per workgroup
@@ -125,8 +126,16 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
     };
     const rsrc_t wsrc0 = make_rsrc(w0, wbytes);
     const rsrc_t wsrc1 = make_rsrc(PAIR ? w1 : w0, wbytes);
-    const rsrc_t xsrc = make_rsrc(x, batch * cols * 2);
     const rsrc_t xssrc = make_rsrc(xsums, 2 * batch * ngroups * 2);
+    // A tile in a 256-token block with a rescaled token reads x from the rescaled copy,
+    // which holds every row of that block, and multiplies its tokens' outputs back by
+    // their factor (TT divides 256).
+    const float *xsb = reinterpret_cast<const float *>(xsums);
+    const XsLayout xl = xs_layout(cols, batch);
+    // (one uniform load; the prologue issues the weight loads before the first x DMA, so
+    // its latency overlaps theirs)
+    const uint32_t tile_scaled = __builtin_amdgcn_readfirstlane(reinterpret_cast<const uint32_t *>(xsb + xl.bflag)[t0 / 256]);
+    const rsrc_t xsrc = make_rsrc(tile_scaled ? static_cast<const void *>(xsb + xl.xcopy) : x, batch * cols * 2);
 
     // byte offset of chunk c of row r, super-block b, in the CDNA4 image
     auto chunk_off = [&](uint32_t r, uint32_t b, uint32_t c) -> uint32_t {
@@ -173,12 +182,10 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
 
     const uint32_t sbeg = 4 * sb0, send = 4 * sb1;
     // prologue: x(sbeg), x(sbeg+1) in LDS; raw(sbeg), raw(sbeg+1) in flight
-    dma_x(sbeg, sbeg % XBUF);
     load_raw(sbeg, raw[0]);
-    if (sbeg + 1 < send) {
-        dma_x(sbeg + 1, (sbeg + 1) % XBUF);
-        load_raw(sbeg + 1, raw[1]);
-    }
+    if (sbeg + 1 < send) load_raw(sbeg + 1, raw[1]);
+    dma_x(sbeg, sbeg % XBUF);
+    if (sbeg + 1 < send) dma_x(sbeg + 1, (sbeg + 1) % XBUF);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
@@ -318,6 +325,18 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
     auto tok_of = [&](int i, int v) -> uint32_t {
         return t0 + uint32_t(i) * 32 + 8 * uint32_t(v >> 2) + 4 * hl + uint32_t(v & 3);
     };
+    // rescaled tokens: times 2^k_t, exact in fp32, so also before the split-K parts are added
+    if (tile_scaled) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const uint32_t t = tok_of(i, v);
+                const float tf = t < batch ? xsb[xl.tfac + t] : 1.f;
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) acc[i][j][v] *= tf;
+            }
+    }
 
     // output of one (token, column pair): fp16 GeGLU (PAIR) or fp32 per column
     auto emit = [&](uint32_t t, const float (&val)[NJ]) {

@@ -92,9 +92,35 @@ void gemv_mt_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, 
 void gemm_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, uint32_t batch, bool pair,
                          const Tuning &t, size_t *floats, size_t *counters);
 
+// What the FP32-mode Q4_K prefill GEMMs read beside x, written by the group-sums
+// kernel, at float offsets from one base (each part starts on a 256-byte boundary):
+//   sums   two fp16 planes [batch][cols/32]: hi and lo of the 32-wide group sums of x
+//   tfac   [batch] fp32: 2^k_t, token t's sums and copied row being those of x_t * 2^-k_t
+//   gflag  [ceil(batch/8)] u32: 1 if any token of that 8-row group has k_t > 0
+//   bflag  [ceil(batch/256)] u32: 1 if any 8-row group of that 256-token block is flagged
+//   xcopy  [batch][cols] fp16: x_t * 2^-k_t for every token of a flagged 256-token block
+// A group sum of 32 fp16 values reaches 32 * 65504; k_t (0 unless token t has a group sum
+// beyond 65504) keeps the fp16 hi of every sum finite.  A GEMM token tile lies inside one
+// 256-token block; in a flagged block it reads x from xcopy and multiplies its tokens'
+// outputs by tfac.
+struct XsLayout {
+    size_t sums, tfac, gflag, bflag, xcopy, total;
+};
+__host__ __device__ inline XsLayout xs_layout(uint32_t cols, uint32_t batch) {
+    auto up64 = [](size_t n) { return (n + 63) / 64 * 64; };
+    XsLayout l;
+    l.sums = 0;
+    l.tfac = up64(size_t(batch) * (cols / 32));
+    l.gflag = l.tfac + up64(batch);
+    l.bflag = l.gflag + up64((size_t(batch) + 7) / 8);
+    l.xcopy = l.bflag + up64((size_t(batch) + 255) / 256);
+    l.total = l.xcopy + up64((size_t(batch) * cols + 1) / 2);
+    return l;
+}
+
 // The Q4_K CDNA4 prefill GEMM with register-resident weight fragments, FP32 mode
-// (ns_gemm_reg.hip): split-K parts it needs, and the launch.  xsums: the two
-// fp16 planes of x group sums; partial: the split-K parts.
+// (ns_gemm_reg.hip): split-K parts it needs, and the launch.  xsums: the base of the
+// XsLayout block; partial: the split-K parts.
 void gemm_reg_workspace_need(uint32_t cols, uint32_t rows, uint32_t batch, bool pair, const Tuning &t,
                              size_t *part_floats, size_t *counters);
 hipError_t launch_gemm_reg(const uint8_t *w, const uint8_t *up, const uint16_t *x, const uint16_t *xsums,
