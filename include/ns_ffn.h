@@ -23,6 +23,19 @@
  *     of an fp32 matmul input above batch 4).  Calls that share
  *     one context must be ordered (one stream, or synchronised); the reference
  *     serialises all GPU work the same way (mm:137).
+ *   - Co-residency.  Three kernels let workgroups wait for other workgroups of the same
+ *     launch: the split-K reduce-scatter finish of the prefill GEMMs (ns_matmul above batch
+ *     4, ns_gate_up_geglu above batch 4, ns_gate_up_geglu_rm32, ns_ffn_down with fp16 input
+ *     above batch 4, ns_qkv above batch 4), the one-launch decode block
+ *     (ns_ffn_block_decode) and the multi-layer decode launch (ns_ffn_stack_decode).  Each
+ *     is launched only when its whole grid fits on the device at once, which guarantees
+ *     progress while nothing else occupies the GPU's compute units.  Work of another stream,
+ *     context or process that holds CUs (in particular a second such kernel launched at the
+ *     same time) can keep part of a grid from being dispatched; every wait is bounded
+ *     (seconds), and a wait that runs out writes that call's affected outputs as NaN and sets
+ *     the context's status word, which ns_ctx_status reports as NS_ERR_TIMEOUT.  An engine
+ *     that shares the GPU calls ns_ctx_set_wait_free(ctx, 1): the same results (bit for bit
+ *     in the FP32 mode) from launches that never wait.
  */
 #ifndef NS_FFN_H
 #define NS_FFN_H
@@ -62,8 +75,9 @@ enum {
     NS_ERR_SHAPE = 2,
     NS_ERR_HIP = 3,
     NS_ERR_UNSUPPORTED = 4,
-    NS_ERR_IO = 5,     /* file create/read/write/mmap failure */
-    NS_ERR_FORMAT = 6  /* .nsmffn file does not validate */
+    NS_ERR_IO = 5,      /* file create/read/write/mmap failure */
+    NS_ERR_FORMAT = 6,  /* .nsmffn file does not validate */
+    NS_ERR_TIMEOUT = 7  /* a bounded cross-workgroup wait ran out (ns_ctx_status) */
 };
 
 typedef struct ns_ctx ns_ctx;
@@ -82,6 +96,17 @@ int ns_abi_version(void);
  * with NS_ERR_UNSUPPORTED while the call's stream is capturing a graph. */
 int ns_ctx_create(int device, ns_ctx **out);
 int ns_ctx_destroy(ns_ctx *ctx);
+/* finish_command (mm:231-243: wait for the command buffer, throw if it failed): waits for
+ * `stream`, then reports whether any work of this context ran a bounded cross-workgroup
+ * wait out since the last report (NS_ERR_TIMEOUT, with the kernel named in ns_last_error();
+ * the word is cleared).  Synchronises; not for use under graph capture. */
+int ns_ctx_status(ns_ctx *ctx, void *stream);
+/* No counterpart in the reference (its GPU is never shared): wait_free != 0 makes every later
+ * call of this context use launches in which no workgroup waits for another (the split-K
+ * GEMMs finish by the last part to arrive; the decode block and the multi-layer decode run
+ * as separate launches), for engines that share the GPU with other work.  Results are
+ * unchanged (the same per-row arithmetic and order). */
+int ns_ctx_set_wait_free(ns_ctx *ctx, int wait_free);
 /* Bytes of device workspace the context holds now. */
 int ns_ctx_workspace_bytes(const ns_ctx *ctx, uint64_t *bytes);
 /* Test and experiment hook, no counterpart in the reference: overrides one
@@ -121,14 +146,21 @@ int ns_matmul(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, u
  * (code under HIP graph capture, serving loops and harnesses that forbid hipMalloc).  The same
  * regimes and kernels as ns_matmul with the default tuning, without a context: the split
  * reductions use a static device scratch array of 16 MiB of parts and 65,536 counters that
- * each GPU holds until the process ends; a shape that needs more fails with
- * NS_ERR_UNSUPPORTED (every decode GEMV and small-batch shape of the reference model fits;
- * large prefill GEMMs do not).  fp32 input above batch 4 is refused (its fp16 copy would need
- * a buffer).  Calls that overlap on
- * one GPU share the array and race: order them (one stream).  Allocates nothing, never
- * synchronises, and may be captured into a graph. */
+ * each GPU holds until the process ends (whether or not it ever calls this function).  A
+ * prefill GEMM (batch > 4) whose default split-K plan needs more parts than the array holds
+ * runs with one K part (the gemm_kparts 1 tuning of ns_matmul: same kernels, one part per
+ * tile, each output within the FP32 tolerance of ns_matmul's); a shape that still needs more
+ * fails with NS_ERR_UNSUPPORTED (a Q4_K GEMM needs ~0.53 floats of scratch per input value:
+ * up to ~2,000 tokens of the 3840-wide gate/up input, ~500 of the 15360-wide down input; Q6_K
+ * none).  fp32 input above batch 4 is refused (its fp16 copy would need a buffer).  Calls
+ * that overlap on one GPU share the array and race: order them (one stream).  Allocates
+ * nothing, never synchronises, and may be captured into a graph. */
 int ns_matmul_noalloc(const void *w, int type, int layout, uint32_t cols, uint32_t rows, uint32_t batch,
                       const void *in, int half_input, float *out, void *stream);
+/* ns_ctx_status for ns_matmul_noalloc on the current device: waits for `stream`, then reports
+ * (NS_ERR_TIMEOUT) and clears a bounded cross-workgroup wait that ran out in the static
+ * scratch's calls since the last report.  Allocates nothing; synchronises. */
+int ns_noalloc_status(void *stream);
 
 /* gate_up_geglu_decode (mm:290): h[r] = gelu_tanh(Wg[r].x) * (Wu[r].x), fp32, Q4_K gate/up. */
 int ns_gate_up_geglu_decode(ns_ctx *ctx, const void *wg, const void *wu, int layout,
@@ -181,6 +213,11 @@ int ns_rmsnorm_add_then(ns_ctx *ctx, const float *x, const float *weight, const 
                         const float *scale, const float *next_weight, uint32_t rows, uint32_t width, float eps,
                         float *y, void *next, int half_next, void *stream);
 
+/* gemma_geglu / gemma_geglu_f16 (metal:530-531; dispatched at mm:568 and mm:570 after two
+ * separate gate and up matmuls): out[i] = gelu_tanh(gate[i]) * up[i] for i < count, fp32 out
+ * or, with half_out, fp16 bits (round to nearest even).  gate and up 16-byte aligned. */
+int ns_geglu(ns_ctx *ctx, const float *gate, const float *up, uint64_t count, void *out, int half_out, void *stream);
+
 /* rms (mm:563, the decode branch) fused into gate_up_geglu_decode (mm:571), one launch:
  * h[r] = gelu_tanh(Wg[r].n) * (Wu[r].n) with n = (x*r)*norm_weight, r = 1/sqrt(mean(x^2) + eps).
  * Q4_K gate/up; cols <= 16384; x and norm_weight 16-byte aligned; fp32 x, h. */
@@ -199,7 +236,8 @@ int ns_rms_gate_up_geglu_decode(ns_ctx *ctx, const void *wg, const void *wu, int
  * tolerance.  y may alias x; h may not overlap either.  x, norm_weight and h 16-byte
  * aligned.  Calls that overlap on one context race (the launch counts its workgroups in
  * the context's workspace).  The one launch's down workgroups wait for the gate/up rows
- * they read, with a bound of seconds: rows of y whose wait ran out are NaN. */
+ * they read, with a bound of seconds: rows of y whose wait ran out are NaN and the
+ * context's status records it (ns_ctx_status; see Co-residency above). */
 int ns_ffn_block_decode(ns_ctx *ctx, const void *wg, const void *wu, const void *wd, int down_type, int layout,
                         uint32_t cols, uint32_t ffn, const float *x, const float *norm_weight, float eps, float *h,
                         float *y, void *stream);

@@ -21,6 +21,9 @@ struct ns_ctx {
     // Buffers replaced by workspace growth.  Work queued earlier, or a graph
     // captured earlier, may still use them, so they live until ns_ctx_destroy.
     std::vector<void *> retired;
+    // Device word the kernels OR a WaitBit into when a bounded cross-workgroup wait runs out
+    // (ws.err points here); read and cleared by ns_ctx_status.
+    uint32_t *err = nullptr;
 };
 
 namespace {
@@ -200,6 +203,13 @@ extern "C" int ns_ctx_create(int device, ns_ctx **out) {
         ns_ctx_destroy(ctx);
         return rc;
     }
+    e = hipMalloc(reinterpret_cast<void **>(&ctx->err), 256);
+    if (e == hipSuccess) e = hipMemset(ctx->err, 0, 256);
+    if (e != hipSuccess) {
+        ns_ctx_destroy(ctx);
+        return hip_fail(e, "ns_ctx_create: status word");
+    }
+    ctx->ws.err = ctx->err;
     e = hipDeviceSynchronize();  // the counters' clear has finished before any stream uses them
     if (e != hipSuccess) {
         ns_ctx_destroy(ctx);
@@ -243,8 +253,44 @@ extern "C" int ns_ctx_destroy(ns_ctx *ctx) {
     if (ctx->ws.partial) (void)hipFree(ctx->ws.partial);
     if (ctx->ws.counters) (void)hipFree(ctx->ws.counters);
     if (ctx->xh) (void)hipFree(ctx->xh);
+    if (ctx->err) (void)hipFree(ctx->err);
     for (void *p : ctx->retired) (void)hipFree(p);
     delete ctx;
+    return NS_OK;
+}
+
+namespace ns {
+// Text of a non-zero status word (WaitBit flags).
+std::string wait_status_message(uint32_t v) {
+    std::string which;
+    const auto add = [&](uint32_t bit, const char *name) {
+        if (!(v & bit)) return;
+        if (!which.empty()) which += ", ";
+        which += name;
+    };
+    add(kWaitGemm, "a prefill GEMM's split-K reduce-scatter");
+    add(kWaitBlock, "the one-launch decode FFN block");
+    add(kWaitStack, "the multi-layer decode launch");
+    return "a cross-workgroup wait ran out in " + which +
+           ": some outputs of that call are NaN (its workgroups were not all resident at once; run with "
+           "ns_ctx_set_wait_free when other work shares the GPU)";
+}
+}  // namespace ns
+
+extern "C" int ns_ctx_status(ns_ctx *ctx, void *stream) {
+    if (!ctx) return fail(NS_ERR_ARG, "ns_ctx_status: null context");
+    hipError_t e = hipSetDevice(ctx->device);
+    uint32_t v = 0;
+    if (e == hipSuccess) e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    if (e == hipSuccess) e = hipMemcpy(&v, ctx->err, sizeof v, hipMemcpyDeviceToHost);
+    if (e == hipSuccess && v != 0) e = hipMemset(ctx->err, 0, sizeof v);
+    if (e != hipSuccess) return hip_fail(e, "ns_ctx_status");
+    return v == 0 ? NS_OK : fail(NS_ERR_TIMEOUT, "ns_ctx_status: " + ns::wait_status_message(v));
+}
+
+extern "C" int ns_ctx_set_wait_free(ns_ctx *ctx, int wait_free) {
+    if (!ctx) return fail(NS_ERR_ARG, "ns_ctx_set_wait_free: null context");
+    ctx->ws.tune.wait_free = wait_free != 0 ? 1 : 0;
     return NS_OK;
 }
 
@@ -370,6 +416,16 @@ extern "C" int ns_rmsnorm_add_then(ns_ctx *ctx, const float *x, const float *wei
     return e == hipSuccess ? NS_OK : hip_fail(e, "ns_rmsnorm_add_then");
 }
 
+extern "C" int ns_geglu(ns_ctx *ctx, const float *gate, const float *up, uint64_t count, void *out, int half_out,
+                        void *stream) {
+    if (!ctx) return fail(NS_ERR_ARG, "ns_geglu: null context");
+    if (!gate || !up || !out) return fail(NS_ERR_ARG, "ns_geglu: null buffer");
+    if ((reinterpret_cast<uintptr_t>(gate) | reinterpret_cast<uintptr_t>(up)) % 16)
+        return fail(NS_ERR_ARG, "ns_geglu: gate and up must be 16-byte aligned");
+    const hipError_t e = launch_geglu(gate, up, count, out, half_out != 0, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? NS_OK : hip_fail(e, "ns_geglu");
+}
+
 namespace {
 int rms_gate_up(ns_ctx *ctx, const char *fn, const void *wg, const void *wu, int layout, uint32_t cols,
                 uint32_t rows, const NormPrologue &np, float *h, void *stream) {
@@ -417,7 +473,8 @@ extern "C" int ns_ffn_block_decode(ns_ctx *ctx, const void *wg, const void *wu, 
     if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(norm_weight) | reinterpret_cast<uintptr_t>(h)) % 16)
         return fail(NS_ERR_ARG, "ns_ffn_block_decode: x, norm_weight and h must be 16-byte aligned");
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (ctx->ws.tune.block_fused != 0 && block_decode_supported(layout, down_type, norm_weight != nullptr, cols, ffn)) {
+    if (ctx->ws.tune.block_fused != 0 && waits_allowed(ctx->ws.tune) &&
+        block_decode_supported(layout, down_type, norm_weight != nullptr, cols, ffn)) {
         size_t pf = 0, nc = 0;
         block_decode_workspace_need(cols, ffn, &pf, &nc);
         if (int rc = ensure_ws(ctx, pf, nc, s)) return rc;

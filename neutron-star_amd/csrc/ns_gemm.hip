@@ -304,7 +304,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
     const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, const uint16_t *__restrict__ x,
     const uint16_t *__restrict__ xsums, void *__restrict__ out, float *__restrict__ partial,
     uint32_t *__restrict__ counters, uint32_t cols, uint32_t rows, uint32_t batch, uint32_t ntok_tiles,
-    uint32_t ncol_tiles, uint32_t kparts_total, uint32_t wbytes, uint32_t rs_spin) {
+    uint32_t ncol_tiles, uint32_t kparts_total, uint32_t wbytes, uint32_t rs_spin, uint32_t *__restrict__ err) {
     constexpr bool Q4 = TYPE == Q4_K;
     constexpr bool F16 = ACC == ACC_FP16;  // fp16 tiles (ns_tile16.hpp) instead of exact ones
     constexpr uint32_t kRawLoads = Q4 ? 2 : (LAYOUT == CDNA4 ? 6 : 41);  // vector loads per load_raw
@@ -674,6 +674,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(
                 __builtin_amdgcn_s_sleep(2);
                 if (++it >= rs_spin) {
                     late = 1;
+                    record_wait_timeout(err, kWaitGemm);
                     break;
                 }
             }
@@ -929,10 +930,11 @@ hipError_t launch_mode(int acc, const uint8_t *w, const uint8_t *up, const uint1
                                         : &gemm_kernel<TYPE, LAYOUT, ACC_FP32, PAIR>;
     // the reduce-scatter needs every part of a tile running at once: the whole grid resident
     uint32_t rs_spin = 0;
-    if (p.kparts > 1 && MI % p.kparts == 0 && ws.tune.gemm_rs != 0 && uint64_t(grid.x) <= resident_wgs(kernel))
+    if (p.kparts > 1 && MI % p.kparts == 0 && ws.tune.gemm_rs != 0 && waits_allowed(ws.tune) &&
+        uint64_t(grid.x) <= resident_wgs(kernel))
         rs_spin = ws.tune.gemm_rs > 1 ? uint32_t(ws.tune.gemm_rs) : 1u << 22;  // 2^22 polls of s_sleep 2: seconds
     kernel<<<grid, block, 0, stream>>>(w, up, x, xh, out, partial, ws.counters, cols, rows, batch, p.ntok, p.ncol,
-                                       p.kparts, wbytes, rs_spin);
+                                       p.kparts, wbytes, rs_spin, ws.err);
     return hipGetLastError();
 }
 
@@ -994,7 +996,8 @@ hipError_t launch_gemm(int type, int layout, int acc, const uint8_t *w, const ui
                        void *out, uint32_t cols, uint32_t rows, uint32_t batch, const Workspace &ws,
                        hipStream_t stream) {
     if (layout == CDNA4 && acc == ACC_FP16)
-        return launch_gemm_f16(type, w, up, x, out, cols, rows, batch, ws.partial, ws.counters, ws.tune, stream);
+        return launch_gemm_f16(type, w, up, x, out, cols, rows, batch, ws.partial, ws.counters, ws.err, ws.tune,
+                               stream);
     uint16_t *xh = nullptr;
     if (type == Q4_K && acc == ACC_FP32) {  // the exact tiles' min term needs the group sums of x
         xh = reinterpret_cast<uint16_t *>(ws.partial);
@@ -1005,7 +1008,8 @@ hipError_t launch_gemm(int type, int layout, int acc, const uint8_t *w, const ui
     }
     const size_t off = xs_floats(type, cols, batch);
     if (use_gemm_reg(type, layout, ws.tune))  // CDNA4 and FP32 mode: the FP16 mode returned above
-        return launch_gemm_reg(w, up, x, xh, out, cols, rows, batch, ws.partial + off, ws.counters, ws.tune, stream);
+        return launch_gemm_reg(w, up, x, xh, out, cols, rows, batch, ws.partial + off, ws.counters, ws.err, ws.tune,
+                               stream);
     if (up) return launch_layout<Q4_K, true>(layout, acc, w, up, x, xh, out, cols, rows, batch, ws, off, stream);
     if (type == Q4_K)
         return launch_layout<Q4_K, false>(layout, acc, w, nullptr, x, xh, out, cols, rows, batch, ws, off, stream);

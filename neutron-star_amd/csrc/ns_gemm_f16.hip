@@ -100,7 +100,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
     const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, const uint16_t *__restrict__ x,
     void *__restrict__ out, float *__restrict__ partial, uint32_t *__restrict__ counters, uint32_t cols,
     uint32_t rows, uint32_t batch, uint32_t ntok_tiles, uint32_t ncol_tiles, uint32_t kparts, uint32_t wbytes,
-    uint32_t rs_spin) {
+    uint32_t rs_spin, uint32_t *__restrict__ err) {
     constexpr bool Q4 = TYPE == Q4_K;
     using Raw = typename std::conditional<Q4, RawQ4, RawQ6>::type;
     // Four separate LDS objects rather than one array: the compiler then sees that a DMA into
@@ -549,6 +549,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(
                 __builtin_amdgcn_s_sleep(2);
                 if (++it >= rs_spin) {
                     late = 1;
+                    record_wait_timeout(err, kWaitGemm);
                     break;
                 }
             }
@@ -696,8 +697,8 @@ void gemm_f16_workspace_need(uint32_t cols, uint32_t rows, uint32_t batch, bool 
 }
 
 hipError_t launch_gemm_f16(int type, const uint8_t *w, const uint8_t *up, const uint16_t *x, void *out, uint32_t cols,
-                           uint32_t rows, uint32_t batch, float *partial, uint32_t *counters, const Tuning &t,
-                           hipStream_t stream) {
+                           uint32_t rows, uint32_t batch, float *partial, uint32_t *counters, uint32_t *err,
+                           const Tuning &t, hipStream_t stream) {
     const bool pair = up != nullptr;
     const F16Plan p = plan_f16(cols, rows, batch, pair, t);
     const dim3 grid(p.ntok * p.ncol * p.kparts), block(kThreads);
@@ -706,10 +707,11 @@ hipError_t launch_gemm_f16(int type, const uint8_t *w, const uint8_t *up, const 
     const auto kernel = pair ? &gemm_f16_kernel<Q4_K, true>
                              : type == Q4_K ? &gemm_f16_kernel<Q4_K, false> : &gemm_f16_kernel<Q6_K, false>;
     uint32_t rs_spin = 0;
-    if (p.kparts > 1 && MI % p.kparts == 0 && t.gemm_rs != 0 && uint64_t(grid.x) <= resident_wgs(kernel))
+    if (p.kparts > 1 && MI % p.kparts == 0 && t.gemm_rs != 0 && waits_allowed(t) &&
+        uint64_t(grid.x) <= resident_wgs(kernel))
         rs_spin = t.gemm_rs > 1 ? uint32_t(t.gemm_rs) : 1u << 22;  // 2^22 polls of s_sleep 2: seconds
     kernel<<<grid, block, 0, stream>>>(w, pair ? up : w, x, out, partial, counters, cols, rows, batch, p.ntok, p.ncol,
-                                       p.kparts, wbytes, rs_spin);
+                                       p.kparts, wbytes, rs_spin, err);
     return hipGetLastError();
 }
 

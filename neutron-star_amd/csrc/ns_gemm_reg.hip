@@ -101,7 +101,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
     const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, const uint16_t *__restrict__ x,
     const uint16_t *__restrict__ xsums, void *__restrict__ out, float *__restrict__ partial,
     uint32_t *__restrict__ counters, uint32_t cols, uint32_t rows, uint32_t batch, uint32_t ntok_tiles,
-    uint32_t ncol_tiles, uint32_t kparts, uint32_t wbytes, uint32_t rs_spin) {
+    uint32_t ncol_tiles, uint32_t kparts, uint32_t wbytes, uint32_t rs_spin, uint32_t *__restrict__ err) {
     __shared__ __attribute__((aligned(16))) u32x4 Xs[XBUF][TT * 8];
     __shared__ uint32_t last_flag, late_flag;
 
@@ -431,6 +431,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_reg_kernel(
                 __builtin_amdgcn_s_sleep(2);
                 if (++it >= rs_spin) {
                     late = 1;
+                    record_wait_timeout(err, kWaitGemm);
                     break;
                 }
             }
@@ -592,7 +593,7 @@ void gemm_reg_workspace_need(uint32_t cols, uint32_t rows, uint32_t batch, bool 
 
 hipError_t launch_gemm_reg(const uint8_t *w, const uint8_t *up, const uint16_t *x, const uint16_t *xsums,
                            void *out, uint32_t cols, uint32_t rows, uint32_t batch, float *partial,
-                           uint32_t *counters, const Tuning &t, hipStream_t stream) {
+                           uint32_t *counters, uint32_t *err, const Tuning &t, hipStream_t stream) {
     const bool pair = up != nullptr;
     const RegPlan p = plan_reg(cols, rows, batch, pair, t);
     const dim3 grid(p.ntok * p.ncol * p.kparts), block(kThreads);
@@ -601,10 +602,10 @@ hipError_t launch_gemm_reg(const uint8_t *w, const uint8_t *up, const uint16_t *
     // the reduce-scatter needs every part of a tile running at once (the whole grid resident) and
     // one token sub-tile per part (its LDS slot)
     uint32_t rs_spin = 0;
-    if (p.kparts == uint32_t(MI) && t.gemm_rs != 0 && uint64_t(grid.x) <= resident_wgs(kernel))
+    if (p.kparts == uint32_t(MI) && t.gemm_rs != 0 && waits_allowed(t) && uint64_t(grid.x) <= resident_wgs(kernel))
         rs_spin = t.gemm_rs > 1 ? uint32_t(t.gemm_rs) : 1u << 22;  // 2^22 polls of s_sleep 2: seconds
     kernel<<<grid, block, 0, stream>>>(w, pair ? up : w, x, xsums, out, partial, counters, cols, rows, batch, p.ntok,
-                                       p.ncol, p.kparts, wbytes, rs_spin);
+                                       p.ncol, p.kparts, wbytes, rs_spin, err);
     return hipGetLastError();
 }
 

@@ -1350,7 +1350,7 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
     const uint8_t *__restrict__ wg, const uint8_t *__restrict__ wu, const uint8_t *__restrict__ wd,
     const float *__restrict__ x, const float *__restrict__ normw, float eps, float *__restrict__ h,
     float *__restrict__ y, uint32_t D, uint32_t F, float *__restrict__ partial, uint32_t *__restrict__ ctr,
-    uint32_t spin_limit) {
+    uint32_t spin_limit, uint32_t *__restrict__ err) {
     __shared__ __attribute__((aligned(16))) float lds_x[kBlockMaxW * kQK];
     __shared__ float lds_part[kBlockMaxW][2][64];
     __shared__ float lds_sum[kBlockMaxW];
@@ -1439,6 +1439,7 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
                 __builtin_amdgcn_s_sleep(1);
                 if (++it >= spin_limit) {
                     __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    record_wait_timeout(err, kWaitBlock);
                     break;
                 }
             }
@@ -1608,12 +1609,15 @@ hipError_t launch_block_decode(int down_type, const uint8_t *wg, const uint8_t *
     // 2^22 polls, each an L2 round trip plus s_sleep 1: seconds
     const uint32_t spin = ws.tune.block_spin > 0 ? uint32_t(ws.tune.block_spin) : 1u << 22;
     const dim3 g(ffn / kRowTile), blk((cols / kQK) * 64);
+    const auto args = [&](auto kernel) {
+        kernel<<<g, blk, 0, stream>>>(wg, wu, wd, x, normw, eps, h, y, cols, ffn, ws.partial, ws.counters, spin, ws.err);
+    };
     if (down_type == Q4_K) {
-        if (normw) block_decode_kernel<Q4_K, true><<<g, blk, 0, stream>>>(wg, wu, wd, x, normw, eps, h, y, cols, ffn, ws.partial, ws.counters, spin);
-        else block_decode_kernel<Q4_K, false><<<g, blk, 0, stream>>>(wg, wu, wd, x, normw, eps, h, y, cols, ffn, ws.partial, ws.counters, spin);
+        if (normw) args(block_kernel_of<Q4_K, true>());
+        else args(block_kernel_of<Q4_K, false>());
     } else {
-        if (normw) block_decode_kernel<Q6_K, true><<<g, blk, 0, stream>>>(wg, wu, wd, x, normw, eps, h, y, cols, ffn, ws.partial, ws.counters, spin);
-        else block_decode_kernel<Q6_K, false><<<g, blk, 0, stream>>>(wg, wu, wd, x, normw, eps, h, y, cols, ffn, ws.partial, ws.counters, spin);
+        if (normw) args(block_kernel_of<Q6_K, true>());
+        else args(block_kernel_of<Q6_K, false>());
     }
     return hipGetLastError();
 }

@@ -29,16 +29,36 @@ struct Tuning {
     int block_fused = 1;  // 0: the decode FFN block as two launches instead of one
     int block_spin = 0;   // > 0: that launch's bound on a down workgroup's wait (polls)
     int gemm_rs = 1;      // 0: split-K FP16-mode GEMMs finish by the last arrival; > 1: reduce-scatter wait bound
+    int wait_free = 0;    // 1 (ns_ctx_set_wait_free): no kernel waits for another workgroup
 };
 
+// Whether a launch may use a cross-workgroup wait at all (the GPU is not declared shared).
+inline bool waits_allowed(const Tuning &t) { return t.wait_free == 0; }
+
+// Kernels whose workgroups wait for each other (the split-K reduce-scatter of the prefill
+// GEMMs, the one-launch decode block, the multi-layer decode launch) bound every wait.  A
+// workgroup whose bound runs out ORs its kernel's bit into the caller's sticky status word,
+// writes its results as NaN and goes on, so the kernel still ends; the host reports the word
+// as an error (ns_ctx_status, ns_noalloc_status).
+enum WaitBit : uint32_t { kWaitGemm = 1u, kWaitBlock = 2u, kWaitStack = 4u };
+
+__device__ __forceinline__ void record_wait_timeout(uint32_t *err, uint32_t bit) {
+    if (err) __hip_atomic_fetch_or(err, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The error text for a non-zero status word.
+std::string wait_status_message(uint32_t v);
+
 // Workspace owned by ns_ctx: fp32 partial sums and per-slab arrival counters
-// for reductions that span workgroups, and the context's tuning.  Counters are
+// for reductions that span workgroups, the sticky status word of timed-out waits
+// (device-visible; nullptr records nothing), and the context's tuning.  Counters are
 // zero between calls (the last workgroup of a slab resets its counter).
 struct Workspace {
     float *partial = nullptr;
     size_t partial_floats = 0;
     uint32_t *counters = nullptr;
     size_t counter_count = 0;
+    uint32_t *err = nullptr;
     Tuning tune;
 };
 
@@ -125,15 +145,15 @@ void gemm_reg_workspace_need(uint32_t cols, uint32_t rows, uint32_t batch, bool 
                              size_t *part_floats, size_t *counters);
 hipError_t launch_gemm_reg(const uint8_t *w, const uint8_t *up, const uint16_t *x, const uint16_t *xsums,
                            void *out, uint32_t cols, uint32_t rows, uint32_t batch, float *partial,
-                           uint32_t *counters, const Tuning &t, hipStream_t stream);
+                           uint32_t *counters, uint32_t *err, const Tuning &t, hipStream_t stream);
 
 // The FP16-mode prefill GEMM on the CDNA4 layout (ns_gemm_f16.hip): fp16 weight
 // tiles with per-row power-of-two scales (ns_tile16.hpp), no x group sums.
 void gemm_f16_workspace_need(uint32_t cols, uint32_t rows, uint32_t batch, bool pair, const Tuning &t,
                              size_t *part_floats, size_t *counters);
 hipError_t launch_gemm_f16(int type, const uint8_t *w, const uint8_t *up, const uint16_t *x, void *out, uint32_t cols,
-                           uint32_t rows, uint32_t batch, float *partial, uint32_t *counters, const Tuning &t,
-                           hipStream_t stream);
+                           uint32_t rows, uint32_t batch, float *partial, uint32_t *counters, uint32_t *err,
+                           const Tuning &t, hipStream_t stream);
 
 // Prefill GEMM over fp16 x [batch][cols]: plain (fp32 out [batch][rows]) or the
 // gate/up pair with GeGLU (fp16 h [batch][rows]).
@@ -154,6 +174,10 @@ hipError_t launch_dequant(int type, int layout, const uint8_t *w, uint32_t cols,
 hipError_t launch_rmsnorm(const float *x, const float *w, const float *residual, const float *scale,
                           const float *next_w, uint32_t rows, uint32_t width, float eps, void *y, bool half_y,
                           void *next, bool half_next, hipStream_t stream);
+
+// gemma_geglu[_f16] (metal:530-531): y[i] = gelu_tanh(g[i]) * u[i], fp32 or fp16 y; g and u
+// 16-byte aligned.
+hipError_t launch_geglu(const float *g, const float *u, uint64_t n, void *y, bool half_out, hipStream_t stream);
 
 // y[i] = fp16(x[i]), round to nearest even; x 16-byte and y 8-byte aligned.
 hipError_t launch_f32_to_f16(const float *x, uint16_t *y, size_t n, hipStream_t stream);

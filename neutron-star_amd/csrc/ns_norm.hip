@@ -1,6 +1,7 @@
-// ns_norm.hip -- the engine's RMSNorm steps around the FFN block (metal:509-529):
-// rms / rms_half, rms_add, rms_add_then_half and its fp32 form, one workgroup
-// per row.
+// ns_norm.hip -- the engine's elementwise steps around the FFN matmuls: the RMSNorm
+// family (metal:509-529: rms / rms_half, rms_add, rms_add_then_half and its fp32 form,
+// one workgroup per row) and the standalone GeGLU (metal:530-531) that follows two
+// separate gate/up matmuls.
 #include <algorithm>
 
 #include "ns_internal.hpp"
@@ -151,6 +152,41 @@ hipError_t launch_rmsnorm(const float *x, const float *w, const float *residual,
     } else {
         rmsnorm_kernel<false, true, true, false><<<g, b, 0, stream>>>(x, w, residual, scale, next_w, width, eps, y, next);
     }
+    return hipGetLastError();
+}
+
+namespace {
+// gemma_geglu / gemma_geglu_f16 (metal:530-531): y[i] = gelu_tanh(g[i]) * u[i], fp32 or fp16
+// (round to nearest even) out.  Four values per thread where the pointers allow it.
+template <bool HALF>
+__global__ __launch_bounds__(kThreads) void geglu_kernel(const float *__restrict__ g, const float *__restrict__ u,
+                                                         uint64_t n, void *__restrict__ y) {
+    const uint64_t i = (uint64_t(blockIdx.x) * kThreads + threadIdx.x) * 4;
+    if (i >= n) return;
+    float v[4];
+    if (i + 4 <= n) {
+        const float4 a = *reinterpret_cast<const float4 *>(g + i), b = *reinterpret_cast<const float4 *>(u + i);
+        v[0] = gelu_tanh(a.x) * b.x;
+        v[1] = gelu_tanh(a.y) * b.y;
+        v[2] = gelu_tanh(a.z) * b.z;
+        v[3] = gelu_tanh(a.w) * b.w;
+    } else {
+        for (uint64_t k = 0; k < 4; ++k) v[k] = i + k < n ? gelu_tanh(g[i + k]) * u[i + k] : 0.f;
+    }
+    for (uint64_t k = 0; k < 4 && i + k < n; ++k) {
+        if constexpr (HALF) reinterpret_cast<_Float16 *>(y)[i + k] = _Float16(v[k]);
+        else reinterpret_cast<float *>(y)[i + k] = v[k];
+    }
+}
+}  // namespace
+
+hipError_t launch_geglu(const float *g, const float *u, uint64_t n, void *y, bool half_out, hipStream_t stream) {
+    if (n == 0) return hipSuccess;
+    if ((reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(u)) % 16) return hipErrorInvalidValue;
+    const uint64_t blocks = (n + 4 * kThreads - 1) / (4 * kThreads);
+    if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
+    if (half_out) geglu_kernel<true><<<dim3(uint32_t(blocks)), dim3(kThreads), 0, stream>>>(g, u, n, y);
+    else geglu_kernel<false><<<dim3(uint32_t(blocks)), dim3(kThreads), 0, stream>>>(g, u, n, y);
     return hipGetLastError();
 }
 

@@ -13,6 +13,10 @@
 // streams, or two threads) race; callers order them.  The counters must start
 // at zero: each call clears the ones it uses with a small kernel before the
 // matmul (stream-ordered, no hipMemsetAsync, so the call can be captured).
+// A prefill GEMM whose default plan (split-K parts padded to whole tiles) does not
+// fit runs with one K part instead (no parts; only the Q4_K group sums of x), as
+// ns_matmul does with the gemm_kparts 1 tuning.  The array also holds a status
+// word for bounded cross-workgroup waits that ran out, read by ns_noalloc_status.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -30,6 +34,7 @@ constexpr size_t kScratchCounters = size_t(1) << 16;
 struct ScratchMem {
     float parts[kScratchFloats];
     uint32_t counters[kScratchCounters];
+    uint32_t err[64];  // err[0]: the WaitBit flags of timed-out waits since the last report
 };
 static __device__ __align__(256) ScratchMem scratch;
 
@@ -95,12 +100,19 @@ extern "C" int ns_matmul_noalloc(const void *w, int type, int layout, uint32_t c
     if (!half_input && batch > 4) return fail(NS_ERR_UNSUPPORTED, std::string(fn) + ": fp32 input above batch 4 (converted to an fp16 copy before the GEMM, a buffer this entry point does not hold) is not offered");
 
     // the same regime split and kernels as ns_matmul (mm:269-275)
-    const Tuning t;
+    Tuning t;
     size_t need_f = 0, need_c = 0;
+    const auto fits = [&] { return need_f <= kScratchFloats && need_c <= kScratchCounters; };
     if (batch == 1) gemv_workspace_need(type, layout, cols, rows, false, t, &need_f, &need_c);
     else if (batch <= 4) gemv_mt_workspace_need(type, layout, cols, rows, false, batch, half_input != 0, t, &need_f, &need_c);
-    else gemm_workspace_need(type, layout, cols, rows, batch, false, t, &need_f, &need_c);
-    if (need_f > kScratchFloats || need_c > kScratchCounters)
+    else {
+        gemm_workspace_need(type, layout, cols, rows, batch, false, t, &need_f, &need_c);
+        if (!fits()) {  // no split-K parts: the GEMM keeps its whole K range per tile
+            t.gemm_kparts = 1;
+            gemm_workspace_need(type, layout, cols, rows, batch, false, t, &need_f, &need_c);
+        }
+    }
+    if (!fits())
         return fail(NS_ERR_UNSUPPORTED, std::string(fn) + ": this shape needs " + std::to_string(need_f * 4) + " B of parts and " +
                                             std::to_string(need_c) + " counters, above the static scratch (" +
                                             std::to_string(kScratchFloats * 4) + " B, " + std::to_string(kScratchCounters) + ")");
@@ -111,6 +123,8 @@ extern "C" int ns_matmul_noalloc(const void *w, int type, int layout, uint32_t c
     ws.partial_floats = kScratchFloats;
     ws.counters = sm->counters;
     ws.counter_count = kScratchCounters;
+    ws.err = sm->err;
+    ws.tune = t;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (need_c) {
         clear_counters<<<dim3(uint32_t((need_c + 255) / 256)), dim3(256), 0, s>>>(ws.counters, uint32_t(need_c));
@@ -122,4 +136,21 @@ extern "C" int ns_matmul_noalloc(const void *w, int type, int layout, uint32_t c
     else if (batch <= 4) e = launch_gemv_mt(type, layout, wb, nullptr, in, half_input != 0, batch, out, cols, rows, ws, s);
     else e = launch_gemm(type, layout, ACC_FP32, wb, nullptr, static_cast<const uint16_t *>(in), out, cols, rows, batch, ws, s);
     return e == hipSuccess ? NS_OK : fail(NS_ERR_HIP, std::string(fn) + ": " + hipGetErrorString(e));
+}
+
+extern "C" int ns_noalloc_status(void *stream) {
+    using namespace ns;
+    ScratchMem *sm = nullptr;
+    if (int rc = scratch_address(&sm)) return rc;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    uint32_t v = 0;
+    hipError_t e = hipStreamSynchronize(s);
+    if (e == hipSuccess) e = hipMemcpy(&v, sm->err, sizeof v, hipMemcpyDeviceToHost);
+    if (e == hipSuccess && v != 0) {
+        clear_counters<<<dim3(1), dim3(64), 0, s>>>(sm->err, 1u);
+        e = hipGetLastError();
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+    }
+    if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("ns_noalloc_status: ") + hipGetErrorString(e));
+    return v == 0 ? NS_OK : fail(NS_ERR_TIMEOUT, "ns_noalloc_status: " + wait_status_message(v));
 }

@@ -111,8 +111,9 @@ public:
     FfnPath(const FfnPath &) = delete;
     FfnPath &operator=(const FfnPath &) = delete;
 
-    // mm:269-275: batch 1 -> dequant-fused GEMV; batch > 1 with fp16 input ->
-    // MFMA GEMM (FP32 accumulation); batch > 1 with fp32 input -> per-token GEMV.
+    // mm:269-275: batch 1 -> dequant-fused GEMV; batch 2-4 -> the small-batch kernels (the
+    // weights streamed once for every token, fp32 or fp16 input); batch > 4 -> MFMA GEMM (FP32
+    // accumulation; fp32 input rounded to fp16 first, as the reference's tile loader does).
     void matmul(hipStream_t e, const Tensor &w, const void *in, float *out, uint32_t batch,
                 bool half_input = false) const {
         check(ns_matmul(ctx_, w_.data(w), int(w.type), int(w_.layout(w)), cols(w), rows(w), batch, in,
@@ -166,14 +167,24 @@ public:
                              static_cast<float *>(mid), out);
             return;
         } else {
-            // mm:570-571: the fused decode kernel; batches of fp32 tokens take it token by token
-            const uint32_t c = cols(gate), r = rows(gate);
-            for (uint32_t t = 0; t < batch; ++t)
-                gate_up_geglu_decode(e, gate, up, static_cast<const float *>(in) + size_t(t) * c,
-                                     static_cast<float *>(mid) + size_t(t) * r);
+            // mm:570: a decode of 2-4 fp32 tokens takes matmul(gate), matmul(up) (the small-batch
+            // kernels, each streaming its weights once for every token) and gemma_geglu into mid
+            same_shape(gate, up);
+            const size_t n = size_t(batch) * rows(gate);
+            float *g = scratch_.gate(n), *u = scratch_.up(n);
+            matmul(e, gate, in, g, batch, false);
+            matmul(e, up, in, u, batch, false);
+            check(ns_geglu(ctx_, g, u, n, mid, 0, e));
         }
         ffn_down(e, down, mid, out, batch, prefill, fast_swa);
     }
+
+    // finish_command (mm:231-243): waits for the work queued on `e` and throws if any call of
+    // this path ran a bounded cross-workgroup wait out (its outputs then hold NaN).
+    void finish(hipStream_t e) const { check(ns_ctx_status(ctx_, e)); }
+    // For engines that share the GPU with other work: launches in which no workgroup waits
+    // for another (ns_ctx_set_wait_free); results are unchanged.
+    void set_wait_free(bool on) { check(ns_ctx_set_wait_free(ctx_, on ? 1 : 0)); }
 
     // The decode block (mm:563 rms when norm_w is given, mm:571-573) in one launch:
     // mid = GeGLU(gate.n, up.n), out = down.mid, n = in or its RMSNorm (norm_w, eps).
@@ -243,8 +254,36 @@ private:
         if (a.shape != b.shape || w_.layout(a) != w_.layout(b))
             throw std::runtime_error("gate and up tensors differ in shape or layout: " + a.name + ", " + b.name);
     }
+    // The engine's separate `gate` and `up` activation buffers (mm:100-101), used by the decode
+    // of 2-4 tokens (mm:570); grown on first use of a larger batch and kept until the path is
+    // destroyed (queued work may still read them).  The first call of a batch size allocates,
+    // so it must not be the one captured into a graph.
+    class Scratch {
+    public:
+        ~Scratch() {
+            for (void *p : bufs_) (void)hipFree(p);
+        }
+        float *gate(size_t n) { return grow(gate_, gate_n_, n); }
+        float *up(size_t n) { return grow(up_, up_n_, n); }
+
+    private:
+        float *grow(float *&p, size_t &have, size_t n) {
+            if (n <= have) return p;
+            void *q = nullptr;
+            if (hipMalloc(&q, n * sizeof(float)) != hipSuccess) throw std::runtime_error("activation buffer allocation failed");
+            bufs_.push_back(q);
+            p = static_cast<float *>(q);
+            have = n;
+            return p;
+        }
+        float *gate_ = nullptr, *up_ = nullptr;
+        size_t gate_n_ = 0, up_n_ = 0;
+        std::vector<void *> bufs_;
+    };
+
     const WeightImage &w_;
     ns_ctx *ctx_ = nullptr;
+    mutable Scratch scratch_;
 };
 
 }  // namespace neutron::amd

@@ -65,8 +65,11 @@ def lib():
             "ns_ctx_destroy": [vp],
             "ns_ctx_workspace_bytes": [vp, ctypes.POINTER(u64)],
             "ns_ctx_set_tuning": [vp, ctypes.c_char_p, i32],
+            "ns_ctx_status": [vp, vp],
+            "ns_ctx_set_wait_free": [vp, i32],
             "ns_matmul": [vp, vp, i32, i32, u32, u32, u32, vp, i32, vp, vp],
             "ns_matmul_noalloc": [vp, i32, i32, u32, u32, u32, vp, i32, vp, vp],
+            "ns_noalloc_status": [vp],
             "ns_gate_up_geglu_decode": [vp, vp, vp, i32, u32, u32, vp, vp, vp],
             "ns_gate_up_geglu_rm32": [vp, vp, vp, i32, u32, u32, u32, vp, vp, i32, vp],
             "ns_gate_up_geglu": [vp, vp, vp, i32, u32, u32, u32, vp, vp, vp],
@@ -76,6 +79,7 @@ def lib():
             "ns_rmsnorm_add": [vp, vp, vp, vp, vp, u32, u32, ctypes.c_float, vp, vp],
             "ns_rmsnorm_add_then": [vp, vp, vp, vp, vp, vp, u32, u32, ctypes.c_float, vp, vp, i32, vp],
             "ns_rms_gate_up_geglu_decode": [vp, vp, vp, i32, u32, u32, vp, vp, ctypes.c_float, vp, vp],
+            "ns_geglu": [vp, vp, vp, u64, vp, i32, vp],
             "ns_ffn_block_decode": [vp, vp, vp, vp, i32, i32, u32, u32, vp, vp, ctypes.c_float, vp, vp, vp],
             "ns_retile": [vp, vp, i32, u32, u32, i32, i32],
             "ns_retile_device": [vp, vp, i32, u32, u32, i32, i32, vp],
@@ -355,6 +359,15 @@ class Context:
         check(lib().ns_ctx_workspace_bytes(self.handle, ctypes.byref(n)))
         return n.value
 
+    def status(self, stream=None):
+        """ns_ctx_status (finish_command, mm:231-243): waits for the stream, raises NsError
+        (NS_ERR_TIMEOUT) when a bounded cross-workgroup wait of this context ran out."""
+        check(lib().ns_ctx_status(self.handle, _stream(stream)))
+
+    def set_wait_free(self, on=True):
+        """ns_ctx_set_wait_free: launches in which no workgroup waits for another."""
+        check(lib().ns_ctx_set_wait_free(self.handle, int(bool(on))))
+
     def __del__(self):
         try:
             self.close()
@@ -395,11 +408,18 @@ class Context:
         elif batch == 1:  # mm:571-573 in one launch (or the same two launches)
             self.ffn_block_decode(gate, up, down, down_type, layout, cols, ffn, inp, mid, out, stream=stream)
             return
-        else:
-            for t in range(batch):
-                self.gate_up_geglu_decode(gate, up, layout, cols, ffn, inp[t * cols:(t + 1) * cols],
-                                          mid[t * ffn:(t + 1) * ffn], stream)
+        else:  # mm:570: matmul(gate), matmul(up) (small-batch kernels), then gemma_geglu
+            import torch
+            g = torch.empty(batch * ffn, dtype=torch.float32, device=mid.device)
+            u = torch.empty(batch * ffn, dtype=torch.float32, device=mid.device)
+            self.matmul(gate, Q4_K, layout, cols, ffn, batch, inp, g, stream=stream)
+            self.matmul(up, Q4_K, layout, cols, ffn, batch, inp, u, stream=stream)
+            self.geglu(g, u, batch * ffn, mid, stream=stream)
         self.ffn_down(down, down_type, layout, ffn, cols, batch, mid, out, prefill, fast, stream)
+
+    def geglu(self, gate, up, count, out, half_out=False, stream=None):
+        """gemma_geglu[_f16] (metal:530-531): out = gelu_tanh(gate) * up, elementwise."""
+        check(lib().ns_geglu(self.handle, _ptr(gate), _ptr(up), count, _ptr(out), int(half_out), _stream(stream)))
 
     def rmsnorm(self, x, weight, rows, width, eps, y, half_out=False, stream=None):
         """rms / rms_half (mm:291-292): y = (x * r) * weight per row."""
@@ -450,6 +470,12 @@ def matmul_noalloc(w, qtype, layout, cols, rows, batch, inp, out, half_input=Fal
     """ns_matmul_noalloc: ns_matmul on the library's static device scratch (no context)."""
     check(lib().ns_matmul_noalloc(_ptr(w), qtype, layout, cols, rows, batch, _ptr(inp), int(half_input), _ptr(out),
                                   _stream(stream)))
+
+
+def noalloc_status(stream=None):
+    """ns_noalloc_status: waits for the stream, raises NsError on a timed-out wait recorded
+    in the static scratch."""
+    check(lib().ns_noalloc_status(_stream(stream)))
 
 
 def retile_device(src, dst, qtype, cols, rows, from_layout, to_layout, stream=None):

@@ -121,6 +121,28 @@ int main() {
     expect(rel_err(y, y_ref, 1, D) <= 1e-3, "decode down GEMV within 1e-3");
     expect(rel_err(l, l_ref, 1, V) <= 1e-3, "lm-head GEMV (row-major) within 1e-3");
 
+    // ---- decode of 2-4 fp32 tokens (mm:570-573): matmul(gate), matmul(up), gemma_geglu, down
+    for (uint32_t bt : {2u, 4u}) {
+        std::vector<float> xb(bt * D);
+        check(ns_synth_normal_f32(24 + bt, 0, bt * D, xb.data(), 4));
+        float *dxb = dev(xb), *dhb = dev(std::vector<float>(bt * F)), *dyb = dev(std::vector<float>(bt * D));
+        path.ffn_block(s, gate, up, down, dxb, dhb, dyb, bt, /*prefill=*/false, /*swa=*/true, /*exact_ffn=*/false);
+        bool threw_status = false;
+        try { path.finish(s); } catch (const std::runtime_error &) { threw_status = true; }
+        expect(!threw_status, "finish() after a decode block reports no timed-out wait");
+        const auto hb = host(dhb, bt * F), yb = host(dyb, bt * D);
+        std::vector<float> hb_ref(bt * F), yb_ref(bt * D);
+        for (uint32_t t = 0; t < bt; ++t) {
+            nso_gate_up_geglu(NSO_ROW_MAJOR, hg.data(), hu.data(), D, F, xb.data() + t * D, hb_ref.data() + t * F, 4);
+            nso_gemv(NSO_Q6_K, NSO_ROW_MAJOR, hd.data(), F, D, hb.data() + t * F, yb_ref.data() + t * D, 4);
+        }
+        expect(rel_err(hb, hb_ref, bt, F) <= 1e-3, bt == 2 ? "decode block, 2 tokens: h within 1e-3" : "decode block, 4 tokens: h within 1e-3");
+        expect(rel_err(yb, yb_ref, bt, D) <= 1e-3, bt == 2 ? "decode block, 2 tokens: y within 1e-3" : "decode block, 4 tokens: y within 1e-3");
+        (void)hipFree(dxb);
+        (void)hipFree(dhb);
+        (void)hipFree(dyb);
+    }
+
     // ---- prefill (mm:563-573), both accumulation modes
     std::vector<uint16_t> xp(B * D);
     check(ns_synth_normal_f16(23, 0, B * D, xp.data(), 4));

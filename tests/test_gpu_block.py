@@ -194,18 +194,28 @@ def test_block_decode_graph_replay(ctx):
 def test_block_decode_bounded_wait(tune, ctx):
     """The down workgroups' wait for h is bounded.  With the bound forced down to one poll
     (from the host: every wave still exits normally), a slab whose wait ran out is written
-    as NaN and every other slab is the normal result; the next launch with the default
-    bound is whole again (the kernel clears its status)."""
+    as NaN and every other slab is the normal result; the context's status reports the
+    timeout exactly when a slab ran out (ns_ctx_status, NS_ERR_TIMEOUT), once; the next
+    launch with the default bound is whole again (the kernel clears its counters) and
+    reports nothing."""
     D, F, dt = 3840, 15360, N.Q6_K
     _, devs = layer(N.layer_seed(0xC0, 0), D, F, dt)
     x = torch.from_numpy(N.synth_normal_f32(0xC1, D)).cuda()
     _, want = run(ctx, devs, dt, D, F, x, None)
+    ctx.status()
     tune("block_spin", 1)
     _, got = run(ctx, devs, dt, D, F, x, None)
+    slabs = got.reshape(-1, 64)
+    ran_out = int(np.isnan(slabs[:, 0]).sum())
+    if ran_out:
+        with pytest.raises(N.NsError, match="decode FFN block") as e:
+            ctx.status()
+        assert e.value.code == 7  # NS_ERR_TIMEOUT
+    ctx.status()  # reported once, then clear
     tune("block_spin", 0)
     _, again = run(ctx, devs, dt, D, F, x, None)
-    slabs = got.reshape(-1, 64)
     for s, row in enumerate(slabs):
         assert np.isnan(row).all() or np.array_equal(row.view(np.uint32), want.reshape(-1, 64)[s].view(np.uint32)), s
-    print(f"bounded wait: {int(np.isnan(slabs[:, 0]).sum())} of {len(slabs)} slabs ran out")
+    print(f"bounded wait: {ran_out} of {len(slabs)} slabs ran out")
     assert np.array_equal(again.view(np.uint32), want.view(np.uint32))
+    ctx.status()

@@ -175,23 +175,31 @@ def test_split_k_reduce_scatter_equals_last_arrival(ctx, tune, mode, qtype, batc
 def test_split_k_reduce_scatter_bounded_wait(ctx, tune, mode, qtype):
     """The reduce-scatter's wait for the other parts is bounded.  Forced down to two polls from
     the host (every wave still exits normally), a part whose wait ran out writes its token
-    sub-tiles (32 tokens each) as NaN and every other sub-tile is the normal result; the next
-    launch with the default bound is whole again (the last part clears the counters)."""
+    sub-tiles (32 tokens each) as NaN and every other sub-tile is the normal result; the
+    context's status reports the timeout (NS_ERR_TIMEOUT) exactly when a sub-tile ran out,
+    once; the next launch with the default bound is whole again (the last part clears the
+    counters) and reports nothing."""
     batch = 1024
     cols, rows, w, xd = _down_case(qtype, batch, 0xE0)
     want = _run_down(ctx, qtype, cols, rows, batch, w, xd, MODES[mode])
+    ctx.status()
     tune("gemm_rs", 2)
     got = _run_down(ctx, qtype, cols, rows, batch, w, xd, MODES[mode])
+    blocks = got.reshape(batch // 32, 32, rows // 256, 256).transpose(0, 2, 1, 3)
+    nan_blocks = int(sum(np.isnan(blocks[a, c]).all() for a in range(blocks.shape[0])
+                         for c in range(blocks.shape[1])))
+    if nan_blocks:
+        with pytest.raises(N.NsError, match="reduce-scatter") as e:
+            ctx.status()
+        assert e.value.code == 7  # NS_ERR_TIMEOUT
+    ctx.status()  # reported once, then clear
     tune("gemm_rs", 1)
     again = _run_down(ctx, qtype, cols, rows, batch, w, xd, MODES[mode])
-    blocks = got.reshape(batch // 32, 32, rows // 256, 256).transpose(0, 2, 1, 3)
     ref = want.reshape(batch // 32, 32, rows // 256, 256).transpose(0, 2, 1, 3)
-    nan_blocks = 0
     for a in range(blocks.shape[0]):
         for c in range(blocks.shape[1]):
-            if np.isnan(blocks[a, c]).all():
-                nan_blocks += 1
-            else:
+            if not np.isnan(blocks[a, c]).all():
                 assert np.array_equal(blocks[a, c].view(np.uint32), ref[a, c].view(np.uint32)), (a, c)
     print(f"bounded wait: {nan_blocks} of {blocks.shape[0] * blocks.shape[1]} sub-tiles ran out")
     assert np.array_equal(again.view(np.uint32), want.view(np.uint32))
+    ctx.status()

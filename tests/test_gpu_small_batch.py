@@ -214,3 +214,46 @@ def test_mfma_fp32_tokens_beyond_fp16_range(ctx, qtype):
     got = y.cpu().numpy()
     for t in range(4):
         assert rel_err(got[t], O.gemv(qtype, O.ROW_MAJOR, host, cols, rows, x[t])) <= TOL32, t
+
+
+@pytest.mark.parametrize("down_type", [N.Q6_K, N.Q4_K], ids=["q6down", "q4down"])
+@pytest.mark.parametrize("batch", [2, 4])
+def test_ffn_block_decode_small_batch_full_size(ctx, batch, down_type):
+    """The FFN block at decode with 2-4 fp32 tokens, at the model's shape (3840 x 15360, CDNA4):
+    matmul(gate) and matmul(up) each stream their weights once for every token, gemma_geglu
+    forms h, then the down projection's small-batch kernel (mm:570-573).  Per token, h against
+    the oracle's gate/up GeGLU and y against the oracle's GEMV of that h, FP32 bar 1e-3."""
+    D, F = 3840, 15360
+    hg, wg = weights(N.Q4_K, 0x70 + batch, F, D, N.CDNA4)
+    hu, wu = weights(N.Q4_K, 0x71 + batch, F, D, N.CDNA4)
+    hd, wd = weights(down_type, 0x72 + batch, D, F, N.CDNA4)
+    xd, xf = tokens(0x73 + batch, batch, D, False)
+    mid = torch.full((batch, F), float("nan"), dtype=torch.float32, device="cuda")
+    out = torch.full((batch, D), float("nan"), dtype=torch.float32, device="cuda")
+    ctx.ffn_block(wg, wu, wd, down_type, N.CDNA4, D, F, batch, xd.reshape(-1), mid.reshape(-1), out.reshape(-1),
+                  prefill=False, swa=True)
+    ctx.status()
+    h = mid.cpu().numpy()
+    y = out.cpu().numpy()
+    for t in range(batch):
+        assert rel_err(h[t], O.gate_up_geglu(O.ROW_MAJOR, hg, hu, D, F, xf[t])) <= TOL32, t
+        assert rel_err(y[t], O.gemv(down_type, O.ROW_MAJOR, hd, F, D, h[t])) <= TOL32, t
+
+
+def test_geglu_elementwise(ctx):
+    """ns_geglu (gemma_geglu / _f16, metal:530-531) against the oracle's GeGLU per element, on a
+    ragged count; fp32 out within 1e-5 of the oracle (the row-max relative error), fp16 out the
+    round-to-nearest-even of the fp32 value."""
+    n = 15360 * 3 + 5
+    g = N.synth_normal_f32(0x80, n) * 3
+    u = N.synth_normal_f32(0x81, n)
+    gd, ud = torch.from_numpy(g).cuda(), torch.from_numpy(u).cuda()
+    y = torch.full((n,), float("nan"), dtype=torch.float32, device="cuda")
+    yh = torch.zeros((n,), dtype=torch.int16, device="cuda")
+    ctx.geglu(gd, ud, n, y)
+    ctx.geglu(gd, ud, n, yh, half_out=True)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    ref = np.array([O.gelu_tanh(float(v)) for v in g], dtype=np.float32) * u
+    assert rel_err(got, ref) <= 1e-5
+    assert np.array_equal(yh.cpu().numpy().view(np.uint16), got.astype(np.float16).view(np.uint16))
