@@ -474,42 +474,66 @@ class Bench:
         xd = torch.empty(D, dtype=torch.float32, device="cuda")
         xd.copy_(self.f32(0x42, D))
         logits = torch.empty(V, dtype=torch.float32, device="cuda")
+        gates, ups, downs = [lay["gate"] for lay in layers], [lay["up"] for lay in layers], [lay["down"] for lay in layers]
+        dtypes = [down_type(l) for l in range(NLAYERS)]
 
-        def decode_step(_i=0):
-            inp = xd
-            for l, lay in enumerate(layers):
-                # rms (mm:563), gate/up + GeGLU and down (mm:571-573): one launch per layer
-                ctx.ffn_block_decode(lay["gate"], lay["up"], lay["down"], down_type(l), N.CDNA4, D, F, inp, h, y,
-                                     norm_weight=norm_w[l], eps=EPS)
-                inp = y
+        def head():
             ctx.rmsnorm(y, norm_w[NLAYERS], 1, D, EPS, xs)  # the output norm ahead of the lm-head (mm:576)
             ctx.matmul(self.lm, Q6, N.CDNA4, D, V, 1, xs, logits)
             xd.copy_(xs)  # the next step starts from this step's final hidden state
 
+        def decode_step(_i=0):
+            # rms (mm:563), gate/up + GeGLU and down (mm:571-573) of all 48 layers: one launch
+            ctx.ffn_stack_decode(gates, ups, downs, dtypes, N.CDNA4, D, F, xd, h, y, norm_weights=norm_w[:NLAYERS],
+                                 eps=EPS)
+            head()
+
+        def decode_step_blocks(_i=0):
+            inp = xd
+            for l, lay in enumerate(layers):  # one launch per layer
+                ctx.ffn_block_decode(lay["gate"], lay["up"], lay["down"], down_type(l), N.CDNA4, D, F, inp, h, y,
+                                     norm_weight=norm_w[l], eps=EPS)
+                inp = y
+            head()
+
         step_bytes = sum(2 * qbytes(Q4, F, D) + qbytes(down_type(l), D, F) for l in range(NLAYERS)) + \
             qbytes(Q6, V, D)
         xd0 = xd.clone()
-        d_ms = self.timed(decode_step, DECODE_STEPS, warm=1)
-        # the same 64 steps replayed from one captured HIP graph of a decode step
-        xd.copy_(xd0)
-        decode_step()
-        torch.cuda.synchronize()
-        eager_logits = logits.clone()
-        graph = torch.cuda.CUDAGraph()
-        xd.copy_(xd0)
-        with torch.cuda.graph(graph):
-            decode_step()
-        xd.copy_(xd0)
-        graph.replay()
-        torch.cuda.synchronize()
-        replay_equal = bool(torch.equal(eager_logits, logits))
-        g_ms = self.timed(lambda i: graph.replay(), DECODE_STEPS, warm=2)
+
+        def measure(step):
+            """eager ms/step, graph ms/step (64 steps replayed from one captured step), and whether
+            the graph's logits equal the eager step's bit for bit."""
+            xd.copy_(xd0)
+            d_ms = self.timed(step, DECODE_STEPS, warm=1)
+            xd.copy_(xd0)
+            step()
+            torch.cuda.synchronize()
+            eager_logits = logits.clone()
+            graph = torch.cuda.CUDAGraph()
+            xd.copy_(xd0)
+            with torch.cuda.graph(graph):
+                step()
+            xd.copy_(xd0)
+            graph.replay()
+            torch.cuda.synchronize()
+            equal = bool(torch.equal(eager_logits, logits))
+            g_ms = self.timed(lambda i: graph.replay(), DECODE_STEPS, warm=2)
+            return d_ms, g_ms, equal, eager_logits
+
+        b_ms, bg_ms, b_equal, b_logits = measure(decode_step_blocks)
+        d_ms, g_ms, replay_equal, s_logits = measure(decode_step)
+        self.ctx.status()
+        same = bool(torch.equal(b_logits, s_logits))
         self.extra.update(cfg4_decode_ms_per_step=round(d_ms, 4), cfg4_decode_graph_ms_per_step=round(g_ms, 4),
                           cfg4_decode_step_bytes=step_bytes,
                           cfg4_decode_graph_GBps=round(step_bytes / (g_ms * 1e-3) / 1e9, 1),
-                          cfg4_graph_replay_bit_exact=replay_equal)
+                          cfg4_graph_replay_bit_exact=replay_equal and b_equal,
+                          cfg4_decode_per_layer_blocks_graph_ms_per_step=round(bg_ms, 4),
+                          cfg4_decode_stack_equals_per_layer_blocks=same)
         log(f"config4 decode: {d_ms:.3f} ms/step eager, {g_ms:.3f} ms/step graph = "
-            f"{step_bytes / (g_ms * 1e-3) / 1e9:.1f} GB/s; graph replay == eager: {replay_equal}")
+            f"{step_bytes / (g_ms * 1e-3) / 1e9:.1f} GB/s (one launch for the 48 layers; one per layer: "
+            f"{b_ms:.3f} eager, {bg_ms:.3f} graph); graph replay == eager: {replay_equal and b_equal}; "
+            f"stack == per-layer blocks: {same}")
 
     # -- PMC driver -----------------------------------------------------------------------
     def pmc_driver(self):

@@ -242,6 +242,23 @@ int ns_ffn_block_decode(ns_ctx *ctx, const void *wg, const void *wu, const void 
                         uint32_t cols, uint32_t ffn, const float *x, const float *norm_weight, float eps, float *h,
                         float *y, void *stream);
 
+/* The decode FFN blocks of n_layers consecutive layers with nothing between them (the engine's
+ * per-layer decode FFN, mm:563-573, repeated; BASELINE's 48-layer FFN stack), in one launch where
+ * the shapes allow it (as ns_ffn_block_decode, with cols/256 < 16), else one ns_ffn_block_decode
+ * per layer.  No single counterpart in the reference.  x_0 = x; for layer l, with n_l = x_l or,
+ * when norm_weights is non-null, (x_l * r) * norm_weights[l] (r = 1/sqrt(mean(x_l^2) + eps)):
+ * h = gelu(Wg[l].n_l) * (Wu[l].n_l), x_{l+1} = Wd[l].h; y = x_{n_layers}.  wg, wu, wd, down_types
+ * and norm_weights are host arrays of n_layers entries (device pointers, NS_TYPE_Q4_K /
+ * NS_TYPE_Q6_K); the table is copied at the call.  Results equal n_layers calls of
+ * ns_ffn_block_decode bit for bit.  h fp32 [ffn] holds the last layer's h; y may alias x; h may
+ * not overlap either.  x, h, y and every norm weight 16-byte aligned.  The launch's workgroups
+ * wait for each other within and across layers (see Co-residency): calls that overlap on one
+ * context race, and a wait that runs out makes y NaN and sets the context's status. */
+int ns_ffn_stack_decode(ns_ctx *ctx, uint32_t n_layers, const void *const *wg, const void *const *wu,
+                        const void *const *wd, const int *down_types, int layout, uint32_t cols, uint32_t ffn,
+                        const float *x, const float *const *norm_weights, float eps, float *h, float *y,
+                        void *stream);
+
 /* gemma_q6k_embedding (metal:503-505; the token embedding at mm:310, scale = sqrt(3840)):
  * out[t][i] = scale * W[ids[t]][i], fp32 [batch][cols], each value as quant.cpp computes it.
  * Q4_K or Q6_K in any layout (the engine may re-tile the embedding for the lm-head GEMV).  An id

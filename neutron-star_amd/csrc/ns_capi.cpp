@@ -148,6 +148,8 @@ void model_workspace_need(const Tuning &t, size_t *floats, size_t *counters) {
     size_t f = 0, c = 0;
     block_decode_workspace_need(3840, 15360, &f, &c);
     take(f, c);
+    stack_decode_workspace_need(3840, 15360, &f, &c);
+    take(f, c);
     *floats = pf;
     *counters = nc;
 }
@@ -242,6 +244,7 @@ extern "C" int ns_ctx_set_tuning(ns_ctx *ctx, const char *key, int value) {
     else if (k == "block_fused") t.block_fused = value;
     else if (k == "block_spin") t.block_spin = value;
     else if (k == "gemm_rs") t.gemm_rs = value;
+    else if (k == "stack_fused") t.stack_fused = value;
     else return fail(NS_ERR_ARG, "ns_ctx_set_tuning: unknown key " + k);
     return NS_OK;
 }
@@ -490,6 +493,50 @@ extern "C" int ns_ffn_block_decode(ns_ctx *ctx, const void *wg, const void *wu, 
         return rc;
     }
     return ns_matmul(ctx, wd, down_type, layout, ffn, cols, 1, h, 0, y, stream);
+}
+
+extern "C" int ns_ffn_stack_decode(ns_ctx *ctx, uint32_t n_layers, const void *const *wg, const void *const *wu,
+                                   const void *const *wd, const int *down_types, int layout, uint32_t cols,
+                                   uint32_t ffn, const float *x, const float *const *norm_weights, float eps, float *h,
+                                   float *y, void *stream) {
+    const char *fn = "ns_ffn_stack_decode";
+    if (!ctx) return fail(NS_ERR_ARG, "ns_ffn_stack_decode: null context");
+    if (n_layers == 0 || !wg || !wu || !wd || !down_types)
+        return fail(NS_ERR_ARG, "ns_ffn_stack_decode: no layers or a null weight table");
+    if (!x || !h || !y) return fail(NS_ERR_ARG, "ns_ffn_stack_decode: null input/output");
+    for (uint32_t l = 0; l < n_layers; ++l) {
+        if (int rc = check_tensor(fn, wg[l], Q4_K, layout, cols, ffn)) return rc;
+        if (int rc = check_tensor(fn, wu[l], Q4_K, layout, cols, ffn)) return rc;
+        if (int rc = check_tensor(fn, wd[l], down_types[l], layout, ffn, cols)) return rc;
+        if (norm_weights && (!norm_weights[l] || reinterpret_cast<uintptr_t>(norm_weights[l]) % 16))
+            return fail(NS_ERR_ARG, "ns_ffn_stack_decode: each norm weight must be non-null and 16-byte aligned");
+    }
+    const auto overlap = [](const void *a, size_t na, const void *b, size_t nb) {
+        const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+        return pa < pb + nb && pb < pa + na;
+    };
+    if (overlap(h, ffn * 4, x, cols * 4)) return fail(NS_ERR_ARG, "ns_ffn_stack_decode: h overlaps x");
+    if (overlap(h, ffn * 4, y, cols * 4)) return fail(NS_ERR_ARG, "ns_ffn_stack_decode: h overlaps y");
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(h)) % 16)
+        return fail(NS_ERR_ARG, "ns_ffn_stack_decode: x, h and y must be 16-byte aligned");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (ctx->ws.tune.stack_fused != 0 && waits_allowed(ctx->ws.tune) &&
+        stack_decode_supported(layout, norm_weights != nullptr, cols, ffn)) {
+        size_t pf = 0, nc = 0;
+        stack_decode_workspace_need(cols, ffn, &pf, &nc);
+        if (int rc = ensure_ws(ctx, pf, nc, s)) return rc;
+        const hipError_t e = launch_stack_decode(n_layers, reinterpret_cast<const uint8_t *const *>(wg),
+                                                 reinterpret_cast<const uint8_t *const *>(wu),
+                                                 reinterpret_cast<const uint8_t *const *>(wd), down_types, x,
+                                                 norm_weights, eps, h, y, cols, ffn, ctx->ws, s);
+        return e == hipSuccess ? NS_OK : hip_fail(e, fn);
+    }
+    // one block per layer, each continuing from the previous one's y in place
+    for (uint32_t l = 0; l < n_layers; ++l)
+        if (int rc = ns_ffn_block_decode(ctx, wg[l], wu[l], wd[l], down_types[l], layout, cols, ffn, l == 0 ? x : y,
+                                         norm_weights ? norm_weights[l] : nullptr, eps, h, y, stream))
+            return rc;
+    return NS_OK;
 }
 
 extern "C" int ns_embedding(ns_ctx *ctx, const void *w, int type, int layout, uint32_t cols, uint32_t rows,

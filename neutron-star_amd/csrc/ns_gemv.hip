@@ -1518,6 +1518,304 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
     }
 }
 
+// ---- the decode FFN blocks of consecutive layers in one launch ---------------------------
+//
+// The block above, looped over the layers of a stack inside one grid: x_{l+1} = y_l, with the
+// RMSNorm of x_l (weight normw[l]) folded into layer l's gate/up dot products.  Between two
+// launches of the block, the next layer's weights start streaming only after the last
+// workgroup has drained, and each launch pays its own ramp.  Here no launch ends between
+// layers: a workgroup requests layer l+1's gate/up weights as soon as it has handed off its
+// layer-l part, while layer l's last slabs are still being finished elsewhere.
+//
+// Workgroup g of NG = F/64 has W = D/256 compute waves (one gate/up super-block and one down
+// super-block each, the block's split) and one control wave (wave W) that does every
+// cross-workgroup step: waits, the combines of the waves' parts, the agent-scope stores of h
+// and of the down parts, arrivals, and the last-arriver sum of y.  Its polls are the only
+// vector memory operations it has in flight, so they never wait for weight data (vector
+// memory operations of a wave complete in order), and it runs at a raised issue priority.
+// Per layer l, five workgroup barriers:
+//   B5  (l > 0) the control wave has handed off layer l-1: the compute waves request layer
+//       l's gate/up weights;
+//   B1  (l > 0) the control wave has seen ydone >= DS*l: every slab of y_{l-1} is written;
+//   B2  every compute wave has its gate/up parts in LDS and has requested its down weights;
+//       the control wave combines them (wave order), stores h (agent scope), counts one
+//       arrival on ready[kq], and waits until ready[kq] >= DS*(l+1);
+//   B3  h's column part kq is complete: the compute waves read it and form their down parts;
+//   B4  the parts are in LDS: the control wave stores the workgroup's down part, counts it
+//       on arrive[dslab] and, as the KQ*(l+1)-th arrival, adds the KQ parts in part order
+//       into y_l and counts ydone; then B5.
+// Counters only grow during a launch (targets scale with l), and the last workgroup to exit
+// resets them.  Buffers are reused across layers safely: y_l's slab s is written only after
+// every workgroup has passed layer l's gate/up (its KQ parts each wait for DS slabs of h,
+// together all NG workgroups), so y may be updated in place and may alias x; h and the parts
+// of layer l+1 are written only after y_l is complete, which needs every read of layer l's h
+// and parts to have happened.  Per row the arithmetic and its order are the block's, so the
+// outputs equal L launches of the block (and so the two-launch form) bit for bit.
+//
+// Progress: as the block, the host launches it only when the whole grid is resident at once.
+// Every wait is bounded: a control wave whose bound runs out sets status and records
+// kWaitStack in err; from then on no control wave waits (each wait also watches status), while
+// every workgroup still counts all its arrivals and exits.  A y slab finished with status set is
+// NaN, and every slab of the last layer is finished after the timed-out wave's arrival, so the
+// whole result is NaN.
+constexpr uint32_t kStackMaxLayers = 64;
+
+template <int T>
+struct DTag {
+    static constexpr int value = T;
+};
+
+struct StackLayers {
+    const uint8_t *wg[kStackMaxLayers];
+    const uint8_t *wu[kStackMaxLayers];
+    const uint8_t *wd[kStackMaxLayers];
+    const float *normw[kStackMaxLayers];
+    uint64_t q6_down;  // bit l: layer l's down projection is Q6_K (else Q4_K)
+};
+
+template <bool NORM>
+__global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) void stack_decode_kernel(
+    const StackLayers layers, uint32_t L, const float *x0, float eps, float *__restrict__ h, float *y, uint32_t D,
+    uint32_t F, float *__restrict__ partial, uint32_t *__restrict__ ctr, uint32_t spin_limit,
+    uint32_t *__restrict__ err) {
+    __shared__ __attribute__((aligned(16))) float lds_x[(kBlockMaxW - 1) * kQK];
+    __shared__ float lds_part[kBlockMaxW - 1][2][64];
+    __shared__ float lds_sum[kBlockMaxW - 1];
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nbg = D / kQK, nbd = F / kQK, KQ = nbd / nbg, DS = D / kRowTile, W = nbg, NG = DS * KQ;
+    const uint32_t g = blockIdx.x, kq = g / DS, dslab = g - kq * DS;
+    // ctr: ydone; status, exits; then ready[KQ] and arrive[DS], each on a line of its own
+    uint32_t *ydone = ctr, *status = ctr + kCtrStride, *exits = ctr + kCtrStride + 1;
+    uint32_t *ready = ctr + 2 * kCtrStride, *arrive = ctr + kCtrStride * (2 + KQ);
+    const auto acknowledged = [] {
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    };
+
+    // The two roles run loops of their own with the same barrier sequence (a barrier counts
+    // waves, wherever in the program they reach it), so no value of one role is live in the
+    // other's code: one shared loop made the compiler spill the compute waves' merged Q6_K
+    // bits around the control code.
+    if (wave == W) {
+        // ---- the control wave ----
+        // Its stores, arrivals and polls share the CU's memory pipeline with the compute waves'
+        // weight loads; at a higher issue priority they are not held behind loads that were
+        // merely ready to issue at the same time (48-layer stack: 27.8 -> 27.3 us per layer).
+        __builtin_amdgcn_s_setprio(3);
+        // Lane 0: once a wait of this or any workgroup has run out (status set), no workgroup
+        // waits any more: the launch drains at once, every later y slab is NaN.  (A workgroup
+        // that stopped waiting runs ahead, and its arrivals can then interleave with another
+        // layer's, so a wait elsewhere might otherwise never see its count.)
+        bool late = false;
+        const auto wait_for = [&](uint32_t *c, uint32_t target) {
+            if (late) return;
+            uint32_t it = 0;
+            while (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+                if (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+                    late = true;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+                if (++it >= spin_limit) {
+                    late = true;
+                    __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    record_wait_timeout(err, kWaitStack);
+                    break;
+                }
+            }
+        };
+        for (uint32_t l = 0; l < L; ++l) {
+            if (l > 0) {  // B1
+                if (lane == 0) wait_for(ydone, DS * l);
+                lds_barrier();
+            }
+            lds_barrier();  // B2: the gate/up parts, wave order
+            float gs = 0.f, us = 0.f;
+            for (uint32_t v = 0; v < W; ++v) {
+                gs += lds_part[v][0][lane];
+                us += lds_part[v][1][lane];
+            }
+            if constexpr (NORM) {
+                float ts = 0.f;
+                for (uint32_t v = 0; v < W; ++v) ts += lds_sum[v];
+                const float rs = rms_factor(ts, D, eps);
+                gs *= rs;
+                us *= rs;
+            }
+            __hip_atomic_store(&h[g * kRowTile + lane], gelu_tanh(gs) * us, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            acknowledged();  // the h stores are acknowledged before the arrival is counted
+            if (lane == 0) {
+                __hip_atomic_fetch_add(&ready[kq * kCtrStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                wait_for(&ready[kq * kCtrStride], DS * (l + 1));
+            }
+            lds_barrier();  // B3: h's column part kq is complete
+            lds_barrier();  // B4: the down parts, wave order
+            float r0 = 0.f;
+            for (uint32_t v = 0; v < W; ++v) r0 += lds_part[v][0][lane];
+            float *dst = partial + (size_t(dslab) * KQ + kq) * 64;
+            __hip_atomic_store(&dst[lane], r0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            acknowledged();
+            uint32_t prev = 0;
+            if (lane == 0)
+                prev = __hip_atomic_fetch_add(&arrive[dslab * kCtrStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            prev = __builtin_amdgcn_readfirstlane(__shfl(prev, 0));
+            if (prev == KQ * (l + 1) - 1) {
+                // the column parts of the slab, loaded 16 at a time and added in part order
+                float sum = 0.f;
+                const float *src = partial + size_t(dslab) * KQ * 64;
+                for (uint32_t q0 = 0; q0 < KQ; q0 += 16) {
+                    float v[16];
+#pragma unroll
+                    for (uint32_t j = 0; j < 16; ++j)
+                        v[j] = __hip_atomic_load(&src[__builtin_elementwise_min(q0 + j, KQ - 1) * 64 + lane],
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                    for (uint32_t j = 0; j < 16; ++j)
+                        if (q0 + j < KQ) sum += v[j];
+                }
+                const bool bad = __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+                __hip_atomic_store(&y[dslab * kRowTile + lane], bad ? __builtin_nanf("") : sum, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                acknowledged();  // y_l's slab is written before it is counted
+                if (lane == 0) __hip_atomic_fetch_add(ydone, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            if (l + 1 < L) lds_barrier();  // B5: the hand-off is done; the next layer's loads may go
+        }
+        // the last workgroup out clears the counters for the next launch (nothing polls them then)
+        if (lane == 0) {
+            const uint32_t done = __hip_atomic_fetch_add(exits, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (done == NG - 1) {
+                __hip_atomic_store(ydone, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(status, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (uint32_t k = 0; k < KQ; ++k)
+                    __hip_atomic_store(&ready[k * kCtrStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (uint32_t s = 0; s < DS; ++s)
+                    __hip_atomic_store(&arrive[s * kCtrStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(exits, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        return;
+    }
+
+    // ---- a compute wave: gate/up super-block `wave` of slab g, down super-block kq*W + wave ----
+    float *xw = lds_x + wave * kQK;  // this wave's 256 inputs
+    const uint32_t b = kq * nbg + wave;
+    // Lane-derived addresses are formed again at each use from an opaque copy of the lane:
+    // hoisted out of the layer loop they would stay live through every layer.
+    const auto opaque_lane = [&] {
+        uint32_t v = lane;
+        asm volatile("" : "+v"(v));
+        return v;
+    };
+    u32x4 cg[2][kQ4Chunks];
+    const auto load_gate_up = [&](uint32_t l) {
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        const uint32_t ln = opaque_lane();
+        q4_load<CDNA4>(layers.wg[l], ln, 0, g, wave, nbg, cg[0]);
+        q4_load<CDNA4>(layers.wu[l], ln, 0, g, wave, nbg, cg[1]);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    };
+    // One layer, per down type: the type branch encloses the whole layer, so that no value
+    // crosses from one layer to the next.  The layer's gate/up weights are requested first,
+    // before the wait for y_{l-1}, once this workgroup's hand-off of layer l-1 is done (B5)
+    // while other workgroups still finish that layer.  Requested at B4 instead, right after
+    // the down dot products, the 270 KB of loads sat ahead of the control wave's part store
+    // in the CU's memory pipeline and its acknowledgement took ~8 us (31.3 against 27.8 us per
+    // layer).  Requested at the end of the previous iteration, they would be live across the
+    // loop's back edge, and the compiler spilled them.
+    const auto layer = [&](uint32_t l, auto tag) {
+        constexpr bool q6 = decltype(tag)::value == Q6_K;
+        const uint8_t *wd = layers.wd[l];
+        if (l > 0) lds_barrier();  // B5: this workgroup's hand-off of layer l-1 is done
+        load_gate_up(l);
+        if (l > 0) lds_barrier();  // B1: y_{l-1} is complete
+        u32x4 c[q6 ? kQ6Chunks : kQ4Chunks];
+        uint32_t m6[q6 ? 64 : 1];
+        {
+            // ---- gate/up slab g, super-block `wave` (the block's step 1) ----
+            const uint32_t lane = opaque_lane();
+            float4 xv;
+            if (l == 0) {
+                xv = reinterpret_cast<const float4 *>(x0 + size_t(wave) * kQK)[lane];
+            } else {
+                const float *xp = y + size_t(wave) * kQK + 4 * lane;
+                xv = float4{__hip_atomic_load(xp + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                            __hip_atomic_load(xp + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                            __hip_atomic_load(xp + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                            __hip_atomic_load(xp + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)};
+            }
+            float4 wv{1.f, 1.f, 1.f, 1.f};
+            if constexpr (NORM) wv = reinterpret_cast<const float4 *>(layers.normw[l] + size_t(wave) * kQK)[lane];
+            const float4 xin = NORM ? float4{xv.x * wv.x, xv.y * wv.y, xv.z * wv.z, xv.w * wv.w} : xv;
+            reinterpret_cast<float4 *>(xw)[lane] = xin;
+            if constexpr (NORM) {
+                float sq = sumsq4(xv, 0.f);
+                for (int m = 32; m >= 1; m >>= 1) sq += __shfl_xor(sq, m);
+                if (lane == 0) lds_sum[wave] = sq;
+            }
+            float xs[8], r[2];
+            group_sums_of<32>(xin, xs);
+            q4_dot<2>(cg, xw, xs, r);
+            lds_part[wave][0][lane] = r[0];
+            lds_part[wave][1][lane] = r[1];
+            // ---- this wave's down weights: slab dslab, part kq, super-block kq*W + wave ----
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            const uint32_t ld = opaque_lane();
+            if constexpr (q6) {
+                // the 13 chunks only: d is read with h
+                const u32x4 *p = reinterpret_cast<const u32x4 *>(wd + region_offset(Q6_K, dslab, b, nbd)) + ld;
+#pragma unroll
+                for (int i = 0; i < int(kQ6Chunks); ++i) c[i] = __builtin_nontemporal_load(p + i * 64);
+            } else {
+                q4_load<CDNA4>(wd, ld, 0, dslab, b, nbd, c);
+            }
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        }
+        lds_barrier();  // B2
+        // the down weights enter the merge only after the barrier: the compiler would otherwise
+        // move the merge (pure arithmetic) above it, and the wave would wait there for its data
+#pragma unroll
+        for (int i = 0; i < int(q6 ? kQ6Chunks : kQ4Chunks); ++i) asm volatile("" : "+v"(c[i]));
+        if constexpr (q6) q6_merge_block(c, m6);  // the six-bit values, while h is being completed
+        lds_barrier();  // B3
+        {
+            // ---- this wave's down part over h's column part kq ----
+            const uint32_t lane = opaque_lane();
+            uint32_t dbits = 0;
+            if constexpr (q6)
+                dbits = reinterpret_cast<const uint16_t *>(wd + region_offset(Q6_K, dslab, b, nbd) + kQ6Chunks * 1024)[lane];
+            const float *hb = h + size_t(b) * kQK + 4 * lane;
+            const float4 hv{__hip_atomic_load(hb + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                            __hip_atomic_load(hb + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                            __hip_atomic_load(hb + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                            __hip_atomic_load(hb + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)};
+            uint32_t lane_b = lane;
+            asm volatile("" : "+v"(lane_b));
+            reinterpret_cast<float4 *>(xw)[lane_b] = hv;
+            float acc;
+            if constexpr (q6) {
+                float xs[16];
+                group_sums_of<16>(hv, xs);
+                acc = q6_dot_merged(m6, c[12], dbits, xw, xs);
+            } else {
+                const u32x4(&cc)[1][kQ4Chunks] = reinterpret_cast<const u32x4(&)[1][kQ4Chunks]>(c);
+                float xs[8], r[1];
+                group_sums_of<32>(hv, xs);
+                q4_dot<1>(cc, xw, xs, r);
+                acc = r[0];
+            }
+            lds_part[wave][0][lane_b] = acc;
+        }
+        lds_barrier();  // B4
+    };
+    for (uint32_t l = 0; l < L; ++l) {
+        if ((layers.q6_down >> l) & 1u) layer(l, DTag<Q6_K>{});
+        else layer(l, DTag<Q4_K>{});
+    }
+}
+
 }  // namespace
 
 void gemv_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, bool pair, const Tuning &t,
@@ -1620,6 +1918,72 @@ hipError_t launch_block_decode(int down_type, const uint8_t *wg, const uint8_t *
         else args(block_kernel_of<Q6_K, false>());
     }
     return hipGetLastError();
+}
+
+// ---- the multi-layer decode launch --------------------------------------------------------
+
+// Workgroups of W compute waves + 1 control wave that a CU holds at once, per device.
+template <bool NORM>
+int stack_wgs_per_cu(uint32_t nbg) {
+    static int cache[64][kBlockMaxW + 1] = {};
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    int &w = cache[dev & 63][nbg];
+    if (w == 0) {
+        int wgs = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&wgs, &stack_decode_kernel<NORM>, int(nbg + 1) * 64, 0) !=
+                hipSuccess || wgs <= 0)
+            wgs = -1;  // unknown: never taken as room
+        w = wgs;
+    }
+    return w;
+}
+
+bool stack_decode_supported(int layout, bool norm, uint32_t cols, uint32_t ffn) {
+    const uint32_t nbg = cols / kQK, nbd = ffn / kQK;
+    if (!(layout == CDNA4 && cols % kQK == 0 && ffn % kQK == 0 && nbg >= 1 && nbg < kBlockMaxW && nbd % nbg == 0))
+        return false;
+    // the whole grid (ffn/64 workgroups) must fit on the device at once
+    const int per_cu = norm ? stack_wgs_per_cu<true>(nbg) : stack_wgs_per_cu<false>(nbg);
+    return per_cu > 0 && uint64_t(ffn / kRowTile) <= uint64_t(per_cu) * uint64_t(device_shape().cus);
+}
+
+void stack_decode_workspace_need(uint32_t cols, uint32_t ffn, size_t *partial_floats, size_t *counters) {
+    const uint32_t KQ = (ffn / kQK) / (cols / kQK), DS = cols / kRowTile;
+    *partial_floats = size_t(DS) * KQ * 64;         // the down projection's column parts
+    *counters = size_t(kCtrStride) * (2 + KQ + DS);  // ydone; status, exits; ready[KQ]; arrive[DS]
+}
+
+hipError_t launch_stack_decode(uint32_t n_layers, const uint8_t *const *wg, const uint8_t *const *wu,
+                               const uint8_t *const *wd, const int *down_types, const float *x,
+                               const float *const *normw, float eps, float *h, float *y, uint32_t cols, uint32_t ffn,
+                               const Workspace &ws, hipStream_t stream) {
+    const bool norm = normw != nullptr;
+    if (n_layers == 0 || !stack_decode_supported(CDNA4, norm, cols, ffn)) return hipErrorInvalidValue;
+    size_t pf = 0, nc = 0;
+    stack_decode_workspace_need(cols, ffn, &pf, &nc);
+    if (ws.partial_floats < pf || ws.counter_count < nc) return hipErrorInvalidValue;
+    // 2^22 polls, each an L2 round trip plus s_sleep 1: seconds
+    const uint32_t spin = ws.tune.block_spin > 0 ? uint32_t(ws.tune.block_spin) : 1u << 22;
+    const dim3 g(ffn / kRowTile), blk((cols / kQK + 1) * 64);
+    // chunks of at most kStackMaxLayers layers (the table is a kernel argument); each chunk
+    // continues from the previous one's y in place
+    for (uint32_t l0 = 0; l0 < n_layers; l0 += kStackMaxLayers) {
+        const uint32_t L = n_layers - l0 < kStackMaxLayers ? n_layers - l0 : kStackMaxLayers;
+        StackLayers t{};
+        for (uint32_t l = 0; l < L; ++l) {
+            t.wg[l] = wg[l0 + l];
+            t.wu[l] = wu[l0 + l];
+            t.wd[l] = wd[l0 + l];
+            t.normw[l] = norm ? normw[l0 + l] : nullptr;
+            if (down_types[l0 + l] == Q6_K) t.q6_down |= uint64_t(1) << l;
+        }
+        const float *xin = l0 == 0 ? x : y;
+        if (norm) stack_decode_kernel<true><<<g, blk, 0, stream>>>(t, L, xin, eps, h, y, cols, ffn, ws.partial, ws.counters, spin, ws.err);
+        else stack_decode_kernel<false><<<g, blk, 0, stream>>>(t, L, xin, eps, h, y, cols, ffn, ws.partial, ws.counters, spin, ws.err);
+        if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 }  // namespace ns

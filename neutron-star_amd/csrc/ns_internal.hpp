@@ -30,6 +30,7 @@ struct Tuning {
     int block_spin = 0;   // > 0: that launch's bound on a down workgroup's wait (polls)
     int gemm_rs = 1;      // 0: split-K FP16-mode GEMMs finish by the last arrival; > 1: reduce-scatter wait bound
     int wait_free = 0;    // 1 (ns_ctx_set_wait_free): no kernel waits for another workgroup
+    int stack_fused = 1;  // 0: the multi-layer decode as one block launch per layer
 };
 
 // Whether a launch may use a cross-workgroup wait at all (the GPU is not declared shared).
@@ -95,6 +96,17 @@ bool block_decode_supported(int layout, int down_type, bool norm, uint32_t cols,
 void block_decode_workspace_need(uint32_t cols, uint32_t ffn, size_t *partial_floats, size_t *counters);
 hipError_t launch_block_decode(int down_type, const uint8_t *wg, const uint8_t *wu, const uint8_t *wd, const float *x,
                                const float *normw, float eps, float *h, float *y, uint32_t cols, uint32_t ffn,
+                               const Workspace &ws, hipStream_t stream);
+
+// The decode FFN blocks of n_layers consecutive layers in one launch (x_{l+1} = y_l, y updated in
+// place), CDNA4 layout, shapes with (ffn/256) a multiple of (cols/256) < 16.  normw non-null:
+// layer l folds the RMSNorm of its input (weight normw[l], eps) into its gate/up dot products.
+// Host arrays of device pointers; down_types[l] is Q4_K or Q6_K.
+bool stack_decode_supported(int layout, bool norm, uint32_t cols, uint32_t ffn);
+void stack_decode_workspace_need(uint32_t cols, uint32_t ffn, size_t *partial_floats, size_t *counters);
+hipError_t launch_stack_decode(uint32_t n_layers, const uint8_t *const *wg, const uint8_t *const *wu,
+                               const uint8_t *const *wd, const int *down_types, const float *x,
+                               const float *const *normw, float eps, float *h, float *y, uint32_t cols, uint32_t ffn,
                                const Workspace &ws, hipStream_t stream);
 
 // Batch 1-4 on the matrix cores (ns_gemv_mfma.hip), CDNA4 layout; launch_gemv_mt routes there

@@ -81,6 +81,7 @@ def lib():
             "ns_rms_gate_up_geglu_decode": [vp, vp, vp, i32, u32, u32, vp, vp, ctypes.c_float, vp, vp],
             "ns_geglu": [vp, vp, vp, u64, vp, i32, vp],
             "ns_ffn_block_decode": [vp, vp, vp, vp, i32, i32, u32, u32, vp, vp, ctypes.c_float, vp, vp, vp],
+            "ns_ffn_stack_decode": [vp, u32, vp, vp, vp, vp, i32, u32, u32, vp, vp, ctypes.c_float, vp, vp, vp],
             "ns_retile": [vp, vp, i32, u32, u32, i32, i32],
             "ns_retile_device": [vp, vp, i32, u32, u32, i32, i32, vp],
             "ns_synth_blocks": [i32, u64, u64, u64, vp, i32],
@@ -450,6 +451,20 @@ class Context:
         check(lib().ns_ffn_block_decode(self.handle, _ptr(wg), _ptr(wu), _ptr(wd), down_type, layout, cols, ffn,
                                         _ptr(x), None if norm_weight is None else _ptr(norm_weight), eps, _ptr(h),
                                         _ptr(y), _stream(stream)))
+
+    def ffn_stack_decode(self, wg, wu, wd, down_types, layout, cols, ffn, x, h, y, norm_weights=None, eps=1e-6,
+                         stream=None):
+        """The decode FFN blocks of len(wg) consecutive layers (mm:563-573 repeated) in one
+        launch: x_{l+1} = Wd[l].(gelu(Wg[l].n_l) * (Wu[l].n_l)), n_l = x_l or its RMSNorm with
+        norm_weights[l]; y = the last layer's output, h its h."""
+        n = len(wg)
+        assert len(wu) == n and len(wd) == n and len(down_types) == n
+        P = ctypes.c_void_p * n
+        tw, tu, td = P(*[_ptr(t) for t in wg]), P(*[_ptr(t) for t in wu]), P(*[_ptr(t) for t in wd])
+        types = (ctypes.c_int * n)(*[int(t) for t in down_types])
+        nws = None if norm_weights is None else P(*[_ptr(t) for t in norm_weights])
+        check(lib().ns_ffn_stack_decode(self.handle, n, tw, tu, td, types, layout, cols, ffn, _ptr(x), nws, eps,
+                                        _ptr(h), _ptr(y), _stream(stream)))
 
     def embedding(self, w, qtype, layout, cols, rows, ids, batch, scale, out, stream=None):
         """gemma_q6k_embedding (metal:503): out[t] = scale * W[ids[t]]."""

@@ -16,7 +16,7 @@ def pytest_configure(config):
 # Defaults of ns_ctx_set_tuning's keys (include/ns_ffn.h).
 TUNING_DEFAULTS = {"gemv_pf": -1, "gemv_waves": 0, "gemv_whole": 1, "gemv_qslab": 1, "gemm_kparts": 0,
                    "gemm_q4_reg": 1, "mt_mfma": 1, "mt_parts": 0, "mt_slabs": 0, "mt_spw": 0, "block_fused": 1,
-                   "block_spin": 0, "gemm_rs": 1}
+                   "block_spin": 0, "gemm_rs": 1, "stack_fused": 1}
 
 
 @pytest.fixture
