@@ -1578,6 +1578,8 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
     const StackLayers layers, uint32_t L, const float *x0, float eps, float *__restrict__ h, float *y, uint32_t D,
     uint32_t F, float *__restrict__ partial, uint32_t *__restrict__ ctr, uint32_t spin_limit,
     uint32_t *__restrict__ err) {
+    // each compute wave's gate super-block of the next layer, DMA'd from HBM (9 KiB a wave)
+    __shared__ __attribute__((aligned(16))) u32x4 lds_gate[kBlockMaxW - 1][kQ4Chunks][64];
     __shared__ __attribute__((aligned(16))) float lds_x[(kBlockMaxW - 1) * kQK];
     __shared__ float lds_part[kBlockMaxW - 1][2][64];
     __shared__ float lds_sum[kBlockMaxW - 1];
@@ -1710,29 +1712,45 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
         return v;
     };
     u32x4 cg[2][kQ4Chunks];
-    const auto load_gate_up = [&](uint32_t l) {
+    const auto load_up = [&](uint32_t l) {
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        const uint32_t ln = opaque_lane();
-        q4_load<CDNA4>(layers.wg[l], ln, 0, g, wave, nbg, cg[0]);
-        q4_load<CDNA4>(layers.wu[l], ln, 0, g, wave, nbg, cg[1]);
+        q4_load<CDNA4>(layers.wu[l], opaque_lane(), 0, g, wave, nbg, cg[1]);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    };
+    // Layer l's gate super-block into this wave's LDS slot by DMA: instruction i writes chunk
+    // i of the 64 rows, lane L's 16 bytes at lds_gate[wave][i][L], the bytes q4_load would put
+    // in lane L's register.  Lane L later reads back only what it wrote itself.
+    const auto dma_gate = [&](uint32_t l) {
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(layers.wg[l]), 0, int(F * nbg * kQ4Bytes), 0x00020000);
+        const uint32_t base = uint32_t(region_offset(Q4_K, g, wave, nbg));
+        const uint32_t vo = opaque_lane() * 16;
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+#pragma unroll
+        for (int i = 0; i < int(kQ4Chunks); ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)&lds_gate[wave][i][0],
+                                                     16, vo, base + uint32_t(i) * 1024, 0, 0);
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
     };
     // One layer, per down type: the type branch encloses the whole layer, so that no value
-    // crosses from one layer to the next.  The layer's gate/up weights are requested first,
-    // before the wait for y_{l-1}, once this workgroup's hand-off of layer l-1 is done (B5)
-    // while other workgroups still finish that layer.  Requested at B4 instead, right after
-    // the down dot products, the 270 KB of loads sat ahead of the control wave's part store
-    // in the CU's memory pipeline and its acknowledgement took ~8 us (31.3 against 27.8 us per
-    // layer).  Requested at the end of the previous iteration, they would be live across the
-    // loop's back edge, and the compiler spilled them.
+    // crosses from one layer to the next.  The layer's gate weights arrive in LDS during layer
+    // l-1's down phase (requested right after this wave's h loads, so they stream while the
+    // down dot products run); its up weights are requested first in the layer, before the
+    // wait for y_{l-1}, once this workgroup's hand-off of layer l-1 is done (B5) while other
+    // workgroups still finish that layer.  Requested at B4 instead, right after the down dot
+    // products, the loads sat ahead of the control wave's part store in the CU's memory
+    // pipeline and its acknowledgement took ~8 us (31.3 against 27.8 us per layer, with both
+    // halves loaded then).  Requested at the end of the previous iteration, register-held
+    // weights would be live across the loop's back edge, and the compiler spilled them.
     const auto layer = [&](uint32_t l, auto tag) {
         constexpr bool q6 = decltype(tag)::value == Q6_K;
         const uint8_t *wd = layers.wd[l];
         if (l > 0) lds_barrier();  // B5: this workgroup's hand-off of layer l-1 is done
-        load_gate_up(l);
+        load_up(l);
         if (l > 0) lds_barrier();  // B1: y_{l-1} is complete
         u32x4 c[q6 ? kQ6Chunks : kQ4Chunks];
         uint32_t m6[q6 ? 64 : 1];
+        uint32_t dbits = 0;
         {
             // ---- gate/up slab g, super-block `wave` (the block's step 1) ----
             const uint32_t lane = opaque_lane();
@@ -1757,6 +1775,13 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
             }
             float xs[8], r[2];
             group_sums_of<32>(xin, xs);
+            // the gate chunks DMA'd into LDS are there once this wave's earlier memory operations
+            // are done (the up weights and x, issued after the DMA, are needed now anyway)
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+#pragma unroll
+            for (int i = 0; i < int(kQ4Chunks); ++i) cg[0][i] = lds_gate[wave][i][lane];
             q4_dot<2>(cg, xw, xs, r);
             lds_part[wave][0][lane] = r[0];
             lds_part[wave][1][lane] = r[1];
@@ -1764,10 +1789,11 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             const uint32_t ld = opaque_lane();
             if constexpr (q6) {
-                // the 13 chunks only: d is read with h
-                const u32x4 *p = reinterpret_cast<const u32x4 *>(wd + region_offset(Q6_K, dslab, b, nbd)) + ld;
+                const uint8_t *base = wd + region_offset(Q6_K, dslab, b, nbd);
+                const u32x4 *p = reinterpret_cast<const u32x4 *>(base) + ld;
 #pragma unroll
                 for (int i = 0; i < int(kQ6Chunks); ++i) c[i] = __builtin_nontemporal_load(p + i * 64);
+                dbits = reinterpret_cast<const uint16_t *>(base + kQ6Chunks * 1024)[ld];
             } else {
                 q4_load<CDNA4>(wd, ld, 0, dslab, b, nbd, c);
             }
@@ -1778,19 +1804,53 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
         // move the merge (pure arithmetic) above it, and the wave would wait there for its data
 #pragma unroll
         for (int i = 0; i < int(q6 ? kQ6Chunks : kQ4Chunks); ++i) asm volatile("" : "+v"(c[i]));
+        if constexpr (q6) asm volatile("" : "+v"(dbits));
         if constexpr (q6) q6_merge_block(c, m6);  // the six-bit values, while h is being completed
         lds_barrier();  // B3
         {
             // ---- this wave's down part over h's column part kq ----
             const uint32_t lane = opaque_lane();
-            uint32_t dbits = 0;
-            if constexpr (q6)
-                dbits = reinterpret_cast<const uint16_t *>(wd + region_offset(Q6_K, dslab, b, nbd) + kQ6Chunks * 1024)[lane];
             const float *hb = h + size_t(b) * kQK + 4 * lane;
-            const float4 hv{__hip_atomic_load(hb + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                            __hip_atomic_load(hb + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                            __hip_atomic_load(hb + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                            __hip_atomic_load(hb + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)};
+            // The h loads and the next layer's gate DMA in one block, which waits for the h loads
+            // only: the DMA streams while this layer's down dot products run.  The compiler does
+            // not see the DMA instructions; had it issued them, its first LDS access after them
+            // (the h values stored below) would wait for all of them, as it cannot tell that they
+            // write other LDS.  Vector memory operations complete in order, so operations the
+            // compiler does not count only make its own later waits stricter; the gate slot is
+            // read after an explicit wait for everything.  After the last layer the same block
+            // runs with a buffer range of 0: the DMA reads are out of range, which reads no
+            // memory and writes zeros to the slot (one block, one wait count, no branch).
+            u32x4 hraw;
+            {
+                const bool next = l + 1 < L;
+                const uint64_t gb = reinterpret_cast<uint64_t>(layers.wg[next ? l + 1 : l]);
+                // buffer resource: base address, stride 0, the range in bytes, the format word
+                const u32x4 rs{uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(gb))),
+                               uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(gb >> 32) & 0xFFFFu)),
+                               uint32_t(__builtin_amdgcn_readfirstlane(next ? F * nbg * kQ4Bytes : 0u)), 0x00020000u};
+                const uint32_t so = __builtin_amdgcn_readfirstlane(uint32_t(region_offset(Q4_K, g, wave, nbg)));
+                const uint32_t lds = __builtin_amdgcn_readfirstlane(
+                    uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) u32x4 *)&lds_gate[wave][0][0])));
+                const uint32_t vo = lane * 16;
+                uint32_t st;
+#define NS_GATE_DMA "s_nop 0\n\tbuffer_load_dwordx4 %[vo], %[rs], %[st] offen lds\n\t"
+#define NS_GATE_NEXT "s_add_u32 m0, m0, 0x400\n\ts_add_u32 %[st], %[st], 0x400\n\t"
+                asm volatile("global_load_dwordx4 %[hv], %[ha], off sc1\n\t"
+                             "s_mov_b32 m0, %[lds]\n\t"
+                             "s_mov_b32 %[st], %[so]\n\t" NS_GATE_DMA NS_GATE_NEXT NS_GATE_DMA NS_GATE_NEXT NS_GATE_DMA
+                                 NS_GATE_NEXT NS_GATE_DMA NS_GATE_NEXT NS_GATE_DMA NS_GATE_NEXT NS_GATE_DMA NS_GATE_NEXT
+                                     NS_GATE_DMA NS_GATE_NEXT NS_GATE_DMA NS_GATE_NEXT NS_GATE_DMA
+                             "s_waitcnt vmcnt(9)"
+                             : [hv] "=&v"(hraw), [st] "=&s"(st)
+                             : [ha] "v"(hb), [rs] "s"(rs), [so] "s"(so), [lds] "s"(lds), [vo] "v"(vo)
+                             : "memory", "m0", "scc");
+#undef NS_GATE_DMA
+#undef NS_GATE_NEXT
+            }
+            // lanes go through a by-value argument: clang's __builtin_bit_cast applied to a lane
+            // of an ext-vector reads lane 0 whatever the lane
+            const auto as_f = [](uint32_t v) { return __builtin_bit_cast(float, v); };
+            const float4 hv{as_f(hraw.x), as_f(hraw.y), as_f(hraw.z), as_f(hraw.w)};
             uint32_t lane_b = lane;
             asm volatile("" : "+v"(lane_b));
             reinterpret_cast<float4 *>(xw)[lane_b] = hv;
@@ -1810,6 +1870,7 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
         }
         lds_barrier();  // B4
     };
+    dma_gate(0);
     for (uint32_t l = 0; l < L; ++l) {
         if ((layers.q6_down >> l) & 1u) layer(l, DTag<Q6_K>{});
         else layer(l, DTag<Q4_K>{});
