@@ -11,15 +11,17 @@ Also reported under "extra":
   config 2  decode FFN block (gate/up Q4_K + GeGLU, down Q6_K), 48 distinct layers;
   config 3  prefill FFN block at batch 1024, both accumulation modes, tokens/s;
   config 4  48-layer FFN stack (Q4_K_M mix), prefill at batch 1024 then 64 decode
-            steps each ending in the lm-head GEMV; the decode step also replayed
-            from a HIP graph;
+            steps each ending in the lm-head GEMV; the 48 decode FFN blocks run as
+            one launch (ns_ffn_stack_decode), and beside it as one launch per layer;
+            each decode step also replayed from a HIP graph;
   batch 2/4 the MTP-verification regime (mm:273, :282): lm-head (fp32 x), gate/up
             pair and Q6_K down (fp16 x), weights streamed once for all tokens;
             beside it, the lm-head as one GEMV per token.
 
 The CPU leg (skipped by --no-cpu) times the oracle on the host cores: config 1 as the
-line's cpu_baseline, and beside configs 0, 2, 3 (both modes) and 4's decode step in
-"extra" (cpu_* keys), each on a bounded sample named in cpu_samples.
+line's cpu_baseline, and beside configs 0, 2, 3 (one whole batch-1024 layer, FP32 mode:
+the reference's CPU path has no FP16-accumulation form) and 4 (decode step and prefill,
+extrapolated from timed parts) in "extra" (cpu_* keys), each sample named in cpu_samples.
 
 Before the W warm-up steps, config-1 steps run untimed for --ramp-ms of wall time (default 300),
 so that the GPU's clock has settled whatever W is.
@@ -322,28 +324,45 @@ class Bench:
         self.extra.update(cpu_cfg2_ffn_block_decode_us=round((t_gu + t_d6) * 1e6, 1),
                           cpu_cfg2_ffn_block_decode_GBps=round(BYTES_FFN_LAYER / (t_gu + t_d6) / 1e9, 3))
         samples["cfg2"] = "one block (gate/up pair then Q6_K down), repeated; per block"
-        # config 3: the prefill block on a sample of tokens, both modes
-        T = 32
-        xs = N.synth_normal_f16(0x66, T * D)
-        hs = N.synth_normal_f16(0x67, T * F)
-        for acc, name in ((0, "fp32acc"), (1, "fp16acc")):
-            t = rate(lambda: (O.gate_up_geglu_prefill(O.ROW_MAJOR, g, u, D, F, T, xs, acc, nthreads=nt),
-                              O.gemm(Q6, O.ROW_MAJOR, d6, F, D, T, hs, acc, nthreads=nt)), 2.0)
-            self.extra[f"cpu_cfg3_prefill_{name}_tokens_per_s"] = round(T / t, 1)
-        samples["cfg3"] = f"{T} of the 1024 tokens through a whole block (gate/up pair then Q6_K down), per mode"
-        # config 4: the decode step = 24 layers with a Q6_K down + 24 with a Q4_K down + the lm-head
+        # config 3: one whole batch-1024 FFN layer (gate/up pair + GeGLU, then the Q6_K down) on the
+        # reference's CPU path, whose arithmetic is the FP32 mode only (quant.cpp:20-21: dequantised
+        # fp32 weights, a sequential fp32 sum); the reference has no CPU form of the FP16 mode.
+        # Timed once, in full: ~2 s on 16 cores.
+        xs = N.synth_normal_f16(0x66, B * D)
+        hs = N.synth_normal_f16(0x67, B * F)
+        t = time.perf_counter()
+        O.gate_up_geglu_prefill(O.ROW_MAJOR, g, u, D, F, B, xs, 0, nthreads=nt)
+        t_gu_pf = time.perf_counter() - t
+        t = time.perf_counter()
+        O.gemm(Q6, O.ROW_MAJOR, d6, F, D, B, hs, 0, nthreads=nt)
+        t_d6_pf = time.perf_counter() - t
+        t3 = t_gu_pf + t_d6_pf
+        self.extra.update(cpu_cfg3_prefill_fp32acc_tokens_per_s=round(B / t3, 1),
+                          cpu_cfg3_prefill_fp32acc_block_s=round(t3, 3))
+        samples["cfg3"] = (f"one whole FFN layer at batch {B} (gate/up pair then Q6_K down), timed once in full; "
+                           "FP32 accumulation, the reference CPU path's only arithmetic")
+        # config 4: the decode step and the 48-layer prefill, extrapolated from the timed parts (a
+        # full CPU run would take ~2.6 s per decode step and ~100 s for the prefill)
         lm = self.lm_host if hasattr(self, "lm_host") else N.synth_weights(Q6, 0x1B, V, D)
         t_lm = rate(lambda: O.gemv(Q6, O.ROW_MAJOR, lm, D, V, x, nthreads=nt), 1.0)
         step = (NLAYERS // 2) * (2 * t_gu + t_d6 + t_d4) + t_lm
-        self.extra.update(cpu_cfg4_decode_ms_per_step=round(step * 1e3, 2))
-        samples["cfg4"] = ("decode step composed of the timed gate/up pair, Q6_K and Q4_K downs and lm-head GEMVs "
-                           "(24 layers of each down type + the lm-head); the RMSNorms are not counted")
+        t = time.perf_counter()
+        O.gemm(Q4, O.ROW_MAJOR, d4, F, D, B, hs, 0, nthreads=nt)
+        t_d4_pf = time.perf_counter() - t
+        prefill = (NLAYERS // 2) * (2 * t_gu_pf + t_d6_pf + t_d4_pf)
+        self.extra.update(cpu_cfg4_decode_ms_per_step_extrapolated=round(step * 1e3, 2),
+                          cpu_cfg4_prefill_s_extrapolated=round(prefill, 2),
+                          cpu_cfg4_prefill_tokens_per_s_extrapolated=round(B / prefill, 2))
+        samples["cfg4"] = ("extrapolated, not run: the decode step from the timed gate/up pair, Q6_K and Q4_K "
+                           "down and lm-head GEMVs (24 layers of each down type + the lm-head); the prefill from "
+                           f"the timed batch-{B} gate/up pair, Q6_K down and Q4_K down (24 layers of each), all in "
+                           "the FP32 mode; RMSNorms not counted")
         self.extra["cpu_cores"] = nt
         self.extra["cpu_model"] = cpu_model()
         self.extra["cpu_samples"] = samples
         log(f"cpu extra: cfg0 {t0 * 1e6:.0f} us, cfg2 {(t_gu + t_d6) * 1e6:.0f} us/block, cfg3 "
-            f"{self.extra['cpu_cfg3_prefill_fp32acc_tokens_per_s']}/{self.extra['cpu_cfg3_prefill_fp16acc_tokens_per_s']}"
-            f" tok/s, cfg4 {step * 1e3:.1f} ms/step")
+            f"{B / t3:.1f} tok/s ({t3:.2f} s for the layer), cfg4 {step * 1e3:.1f} ms/step and {prefill:.1f} s prefill "
+            "(extrapolated)")
 
     # -- config 0 and 3 ------------------------------------------------------------
     def config0(self):

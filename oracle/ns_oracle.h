@@ -26,9 +26,13 @@
  *     roundings of A, B and F, subnormal B, the row scale's ceil(log2 M) at and
  *     just past powers of two, M = 0) and the output schedule against known
  *     answers (integer sums 2049 -> 2048 in one block, 2049 + 1 over two blocks
- *     -> 2050: one rounding at the end, none per block).  What stays unpinned is
- *     the reference's own FP16 arithmetic on Apple simdgroup_half8x8 hardware,
- *     which runs nowhere here; this mode is within 1e-2 of the FP32 path.
+ *     -> 2050: one rounding at the end, none per block).  These functions restate
+ *     this build's own FP16-mode tiles and rounding, so a kernel checked against
+ *     them is checked for self-consistency, not against the reference.  Parity
+ *     unpinned: the reference's own FP16 arithmetic on Apple simdgroup_half8x8
+ *     hardware, which runs nowhere here (it accumulates in half and has no single
+ *     final rounding).  The FP16 mode's parity evidence is its 1e-2 bound against
+ *     the FP32 path (acc_mode 0, the reference's CPU arithmetic).
  */
 #ifndef NS_ORACLE_H
 #define NS_ORACLE_H

@@ -217,8 +217,11 @@ def test_prefill_small_batch_takes_fp32_kernels(ctx, batch):
 def test_prefill_48_layers_full_size_finite(ctx):
     """Config 4's prefill at full size: 48 distinct seeded layers at batch 1024 with the
     Q4_K_M down mix and the mode rule (layers 5, 11, ... FP32, the rest FP16), chained through
-    rms_half with seeded sign weights.  Every layer's Y must be finite and non-zero, and the
-    first two layers' outputs are checked against the oracle on 64-row samples."""
+    rms_half with seeded sign weights.  Every layer's Y must be finite and non-zero.  Layers 0
+    and 1 (FP16 mode, Q6_K and Q4_K down), 5 (FP32 mode, Q4_K down) and 8 (FP16 mode, Q6_K down,
+    deep in the chain) are checked on 64-row samples of H and Y (all 1024 tokens) against the
+    oracle in the layer's own mode and against the FP32 oracle (the reference's CPU arithmetic)
+    at north_star's bars: 1e-3 in the FP32 mode, 1e-2 in the FP16 mode."""
     D, F, B = 3840, 15360, 1024
     x = torch.from_numpy(N.synth_normal_f16(0x48, B * D).view(np.int16).reshape(B, D)).cuda()
     hp = torch.empty((B, F), dtype=torch.int16, device="cuda")
@@ -233,15 +236,32 @@ def test_prefill_48_layers_full_size_finite(ctx):
         ctx.ffn_block(wg, wu, wd, dt, N.CDNA4, D, F, B, x, hp, yp, prefill=True, swa=not glob)
         torch.cuda.synchronize()
         assert torch.isfinite(yp).all() and torch.any(yp != 0), layer
-        if layer < 2:
+        if layer in (0, 1, 5, 8):
+            # rel_err's denominator is the max of a token's whole output row (15360 values of H,
+            # 3840 of Y); for a 64-column sample it is taken from the GPU's full row, which
+            # equals the oracle's to within the error measured.  The max over the 64 sampled
+            # values alone can be small for a token (H 2.6e-2 on layer 1 against ~1e-3 on the
+            # whole row): that would test the sample, not the metric.
             xh = x.cpu().numpy().view(np.uint16)
             hh = hp.cpu().numpy().view(np.uint16)
+            hfull = f16_value(hh)
+            yfull = yp.cpu().numpy()
+
+            def row_err(got, ref, full):
+                num = np.max(np.abs(got.astype(np.float64) - ref), axis=1)
+                return float(np.max(num / np.max(np.abs(full.astype(np.float64)), axis=1)))
+
             mode = 0 if glob else 1
+            bar = TOL32 if glob else TOL16
             gs = hg.reshape(F, -1)[:64].reshape(-1)
             us = hu.reshape(F, -1)[:64].reshape(-1)
-            assert rel_err(f16_value(hh[:, :64]), O.gate_up_geglu_prefill(O.ROW_MAJOR, gs, us, D, 64, B, xh, mode)) <= 5e-3
+            hgot = hfull[:, :64]
+            assert row_err(hgot, O.gate_up_geglu_prefill(O.ROW_MAJOR, gs, us, D, 64, B, xh, mode), hfull) <= 5e-3, layer
+            assert row_err(hgot, O.gate_up_geglu_prefill(O.ROW_MAJOR, gs, us, D, 64, B, xh, 0), hfull) <= bar, layer
             ds = hd.reshape(D, -1)[:64].reshape(-1)
-            assert rel_err(yp.cpu().numpy()[:, :64], O.gemm(dt, O.ROW_MAJOR, ds, F, 64, B, hh, mode)) <= 1e-3
+            ygot = yfull[:, :64]
+            assert row_err(ygot, O.gemm(dt, O.ROW_MAJOR, ds, F, 64, B, hh, mode), yfull) <= 1e-3, layer
+            assert row_err(ygot, O.gemm(dt, O.ROW_MAJOR, ds, F, 64, B, hh, 0), yfull) <= bar, layer
         nw = signs(N.layer_seed(0xC4, layer + 1) + 5, D)
         xn = torch.empty((B, D), dtype=torch.int16, device="cuda")
         ctx.rmsnorm(yp, torch.from_numpy(nw).cuda(), B, D, EPS, xn, half_out=True)

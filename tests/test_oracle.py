@@ -9,8 +9,17 @@ Pins, per oracle function:
   gemv           bit-identical to dot_row for every row.
   gelu_tanh      gelu(0)=0, gelu(g)-gelu(-g)=g, large |g| -> relu, float64 formula.
   .nsmffn index  metal_ffn.cpp:145-146 known answers and bijection.
-  FP16 mode      no reference can run (Apple half accumulators): only bounded
-                 against the FP32 mode -- parity unpinned beyond that.
+  FP16 mode      the oracle's FP16-mode functions (f16_tile_rows, gemm and
+                 gate_up_geglu_prefill with acc_mode 1) restate this build's own
+                 tile formulas and its single final rounding, so checks against
+                 them are a self-consistency check of the kernels.  They are pinned
+                 here by worked tile values, equality with the reference's
+                 half(d*sc*q - dmin*m) form on power-of-two factors, the tile error
+                 bound and the 2049+1 rounding case.  The reference's own FP16 mode
+                 accumulates in Apple simdgroup half registers (metal:380, :487),
+                 which nothing here can run: parity with that arithmetic is
+                 unpinned.  The FP16 mode's parity evidence is its bound against
+                 the FP32 oracle (the reference's CPU arithmetic), 1e-2.
 """
 import os
 
