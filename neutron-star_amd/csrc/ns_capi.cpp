@@ -24,6 +24,9 @@ struct ns_ctx {
     // Device word the kernels OR a WaitBit into when a bounded cross-workgroup wait runs out
     // (ws.err points here); read and cleared by ns_ctx_status.
     uint32_t *err = nullptr;
+    // The multi-layer decode launch's epoch and tagged h / y (one allocation).
+    ns::StackBuffers stack;
+    void *stack_mem = nullptr;
 };
 
 namespace {
@@ -91,6 +94,38 @@ int ensure_ws(ns_ctx *ctx, size_t partial_floats, size_t counters, hipStream_t s
         ctx->ws.counters = c;
         ctx->ws.counter_count = counters;
     }
+    return NS_OK;
+}
+
+// Makes the context's multi-layer decode buffers fit cols x ffn, on the same terms as ensure_ws
+// (growth retires the old allocation and is refused during stream capture).  A new allocation is
+// zeroed and its epoch set to 1, synchronously: no tag of zeroed memory is ever current.
+int ensure_stack(ns_ctx *ctx, uint32_t cols, uint32_t ffn, hipStream_t s) {
+    StackBuffers &sb = ctx->stack;
+    if (sb.epoch && cols <= sb.cols && ffn <= sb.ffn) return NS_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (s && hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+        return fail(NS_ERR_UNSUPPORTED, "decode buffer growth during stream capture: run the shape once before capturing");
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return hip_fail(e, "decode buffer growth");
+    const uint32_t c = std::max(cols, sb.cols), f = std::max(ffn, sb.ffn);
+    const size_t bytes = 256 + (size_t(f) + c) * sizeof(uint64_t);
+    void *p = nullptr;
+    e = hipMalloc(&p, bytes);
+    if (e == hipSuccess) e = hipMemset(p, 0, bytes);
+    const uint32_t one = 1;
+    if (e == hipSuccess) e = hipMemcpy(p, &one, sizeof one, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        if (p) (void)hipFree(p);
+        return hip_fail(e, "decode buffer allocation");
+    }
+    if (ctx->stack_mem) ctx->retired.push_back(ctx->stack_mem);
+    ctx->stack_mem = p;
+    sb.epoch = static_cast<uint32_t *>(p);
+    sb.htag = reinterpret_cast<uint64_t *>(static_cast<char *>(p) + 256);
+    sb.ytag = sb.htag + f;
+    sb.cols = c;
+    sb.ffn = f;
     return NS_OK;
 }
 
@@ -212,6 +247,11 @@ extern "C" int ns_ctx_create(int device, ns_ctx **out) {
         return hip_fail(e, "ns_ctx_create: status word");
     }
     ctx->ws.err = ctx->err;
+    // the multi-layer decode buffers for the reference model's shape (model.cpp:14-19)
+    if (int rc = ensure_stack(ctx, 3840, 15360, nullptr)) {
+        ns_ctx_destroy(ctx);
+        return rc;
+    }
     e = hipDeviceSynchronize();  // the counters' clear has finished before any stream uses them
     if (e != hipSuccess) {
         ns_ctx_destroy(ctx);
@@ -257,6 +297,7 @@ extern "C" int ns_ctx_destroy(ns_ctx *ctx) {
     if (ctx->ws.counters) (void)hipFree(ctx->ws.counters);
     if (ctx->xh) (void)hipFree(ctx->xh);
     if (ctx->err) (void)hipFree(ctx->err);
+    if (ctx->stack_mem) (void)hipFree(ctx->stack_mem);
     for (void *p : ctx->retired) (void)hipFree(p);
     delete ctx;
     return NS_OK;
@@ -525,10 +566,11 @@ extern "C" int ns_ffn_stack_decode(ns_ctx *ctx, uint32_t n_layers, const void *c
         size_t pf = 0, nc = 0;
         stack_decode_workspace_need(cols, ffn, &pf, &nc);
         if (int rc = ensure_ws(ctx, pf, nc, s)) return rc;
+        if (int rc = ensure_stack(ctx, cols, ffn, s)) return rc;
         const hipError_t e = launch_stack_decode(n_layers, reinterpret_cast<const uint8_t *const *>(wg),
                                                  reinterpret_cast<const uint8_t *const *>(wu),
                                                  reinterpret_cast<const uint8_t *const *>(wd), down_types, x,
-                                                 norm_weights, eps, h, y, cols, ffn, ctx->ws, s);
+                                                 norm_weights, eps, h, y, cols, ffn, ctx->ws, ctx->stack, s);
         return e == hipSuccess ? NS_OK : hip_fail(e, fn);
     }
     // one block per layer, each continuing from the previous one's y in place

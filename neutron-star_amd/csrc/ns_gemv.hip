@@ -1524,40 +1524,52 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
 // RMSNorm of x_l (weight normw[l]) folded into layer l's gate/up dot products.  Between two
 // launches of the block, the next layer's weights start streaming only after the last
 // workgroup has drained, and each launch pays its own ramp.  Here no launch ends between
-// layers: a workgroup requests layer l+1's gate/up weights as soon as it has handed off its
-// layer-l part, while layer l's last slabs are still being finished elsewhere.
+// layers, and the weights of the next layer stream while this one finishes.
 //
 // Workgroup g of NG = F/64 has W = D/256 compute waves (one gate/up super-block and one down
-// super-block each, the block's split) and one control wave (wave W) that does every
-// cross-workgroup step: waits, the combines of the waves' parts, the agent-scope stores of h
-// and of the down parts, arrivals, and the last-arriver sum of y.  Its polls are the only
-// vector memory operations it has in flight, so they never wait for weight data (vector
-// memory operations of a wave complete in order), and it runs at a raised issue priority.
-// Per layer l, five workgroup barriers:
+// super-block each, the block's split) and one control wave (wave W) that combines the waves'
+// parts and hands them to other workgroups.
+//
+// Hand-off by tagged values.  Every value of h and of the intermediate y is stored together
+// with a tag, the launch's epoch * 64 + layer + 1, as one 64-bit agent-scope store; a reader
+// loads the 64-bit words and re-reads until every tag is the one it needs.  So no counter has
+// to be acknowledged, counted and polled before data moves on: a reader's first loads are
+// issued right after the weight loads it needs anyway, complete in order behind them, and
+// find the values there in the common case.  The epoch lives in a buffer of its own that the
+// launch's last workgroup advances, so a word left by an earlier launch (or zeroed at
+// allocation: tag 0, the epoch starts at 1) never carries a current tag, also across graph
+// replays.  Only y's column parts still meet by the last-arriver hand-off (arrive[dslab]).
+//
+// Per layer l, four workgroup barriers:
 //   B5  (l > 0) the control wave has handed off layer l-1: the compute waves request layer
-//       l's gate/up weights;
-//   B1  (l > 0) the control wave has seen ydone >= DS*l: every slab of y_{l-1} is written;
-//   B2  every compute wave has its gate/up parts in LDS and has requested its down weights;
-//       the control wave combines them (wave order), stores h (agent scope), counts one
-//       arrival on ready[kq], and waits until ready[kq] >= DS*(l+1);
-//   B3  h's column part kq is complete: the compute waves read it and form their down parts;
-//   B4  the parts are in LDS: the control wave stores the workgroup's down part, counts it
-//       on arrive[dslab] and, as the KQ*(l+1)-th arrival, adds the KQ parts in part order
-//       into y_l and counts ydone; then B5.
-// Counters only grow during a launch (targets scale with l), and the last workgroup to exit
-// resets them.  Buffers are reused across layers safely: y_l's slab s is written only after
-// every workgroup has passed layer l's gate/up (its KQ parts each wait for DS slabs of h,
-// together all NG workgroups), so y may be updated in place and may alias x; h and the parts
-// of layer l+1 are written only after y_l is complete, which needs every read of layer l's h
-// and parts to have happened.  Per row the arithmetic and its order are the block's, so the
-// outputs equal L launches of the block (and so the two-launch form) bit for bit.
+//       l's up weights (the gate weights came into LDS by DMA during layer l-1's down phase,
+//       see below), then read x_l = y_{l-1} (tags of layer l-1) and form the gate/up parts;
+//   B2  the parts are in LDS and every compute wave has requested its down weights; the
+//       control wave combines them (wave order) and stores h tagged;
+//   B3  the control wave's reads of the parts are done; the compute waves read their 256
+//       values of h (tags of layer l), request the next layer's gate weights into LDS and form
+//       their down parts;
+//   B4  the down parts are in LDS: the control wave stores the workgroup's part, counts it on
+//       arrive[dslab] and, as the KQ*(l+1)-th arrival, adds the KQ parts in part order into
+//       y_l (tagged; the caller's y, plainly, after the last layer); then B5.
+// The gate DMA and the up loads stay out of the control wave's way: the DMA is requested
+// after the compute waves' h loads and streams during the down dot products; the up loads
+// wait for B5, since requested at B4 the loads sat ahead of the control wave's part store in
+// the CU's memory pipeline (its acknowledgement took ~8 us).
+//
+// Buffers are reused across layers safely: layer l+1 writes h and the column parts only after
+// reading x_{l+1}, which is complete only after every workgroup has formed its layer-l down
+// part (so has read h_l), and y_{l+1}'s slab s only after every workgroup has passed layer
+// l+1's gate/up (its KQ parts each read h of DS slabs, together all NG workgroups), so after
+// every read of y_l.  Per row the arithmetic and its order are the block's, so the outputs
+// equal L launches of the block (and so the two-launch form) bit for bit.
 //
 // Progress: as the block, the host launches it only when the whole grid is resident at once.
-// Every wait is bounded: a control wave whose bound runs out sets status and records
-// kWaitStack in err; from then on no control wave waits (each wait also watches status), while
-// every workgroup still counts all its arrivals and exits.  A y slab finished with status set is
-// NaN, and every slab of the last layer is finished after the timed-out wave's arrival, so the
-// whole result is NaN.
+// Every read of tagged values is bounded: a compute wave whose bound runs out sets status and
+// records kWaitStack in err; from then on no wave waits (each wait also watches status), and
+// every workgroup still does all its steps and exits.  A y slab finished with status set is
+// NaN, and every slab of the last layer is finished after the timed-out wave's workgroup has
+// counted its last part, so the whole result is NaN.
 constexpr uint32_t kStackMaxLayers = 64;
 
 template <int T>
@@ -1573,11 +1585,22 @@ struct StackLayers {
     uint64_t q6_down;  // bit l: layer l's down projection is Q6_K (else Q4_K)
 };
 
+// A value and its tag as one 64-bit word, stored and loaded at agent scope.
+__device__ __forceinline__ void store_tagged(uint64_t *p, float v, uint32_t tag) {
+    __hip_atomic_store(p, uint64_t(__builtin_bit_cast(uint32_t, v)) | (uint64_t(tag) << 32), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t load_tagged(const uint64_t *p) {
+    return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float tagged_value(uint64_t w) { return __builtin_bit_cast(float, uint32_t(w)); }
+__device__ __forceinline__ uint32_t tagged_tag(uint64_t w) { return uint32_t(w >> 32); }
+
 template <bool NORM>
 __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) void stack_decode_kernel(
     const StackLayers layers, uint32_t L, const float *x0, float eps, float *__restrict__ h, float *y, uint32_t D,
-    uint32_t F, float *__restrict__ partial, uint32_t *__restrict__ ctr, uint32_t spin_limit,
-    uint32_t *__restrict__ err) {
+    uint32_t F, float *__restrict__ partial, uint32_t *__restrict__ ctr, uint32_t *__restrict__ epoch,
+    uint64_t *__restrict__ htag, uint64_t *__restrict__ ytag, uint32_t spin_limit, uint32_t *__restrict__ err) {
     // each compute wave's gate super-block of the next layer, DMA'd from HBM (9 KiB a wave)
     __shared__ __attribute__((aligned(16))) u32x4 lds_gate[kBlockMaxW - 1][kQ4Chunks][64];
     __shared__ __attribute__((aligned(16))) float lds_x[(kBlockMaxW - 1) * kQK];
@@ -1587,9 +1610,12 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t nbg = D / kQK, nbd = F / kQK, KQ = nbd / nbg, DS = D / kRowTile, W = nbg, NG = DS * KQ;
     const uint32_t g = blockIdx.x, kq = g / DS, dslab = g - kq * DS;
-    // ctr: ydone; status, exits; then ready[KQ] and arrive[DS], each on a line of its own
-    uint32_t *ydone = ctr, *status = ctr + kCtrStride, *exits = ctr + kCtrStride + 1;
-    uint32_t *ready = ctr + 2 * kCtrStride, *arrive = ctr + kCtrStride * (2 + KQ);
+    // ctr: status, exits; then arrive[DS], each on a line of its own
+    uint32_t *status = ctr, *exits = ctr + 1, *arrive = ctr + kCtrStride;
+    // the launch's epoch: read by every wave before any workgroup can have exited (the last one
+    // out advances it)
+    const uint32_t E = __builtin_amdgcn_readfirstlane(__hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    const auto tag_of = [&](uint32_t l) { return E * 64u + l + 1u; };
     const auto acknowledged = [] {
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __builtin_amdgcn_s_waitcnt(0);
@@ -1602,37 +1628,13 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
     // bits around the control code.
     if (wave == W) {
         // ---- the control wave ----
-        // Its stores, arrivals and polls share the CU's memory pipeline with the compute waves'
-        // weight loads; at a higher issue priority they are not held behind loads that were
-        // merely ready to issue at the same time (48-layer stack: 27.8 -> 27.3 us per layer).
+        // Its stores and arrivals share the CU's memory pipeline with the compute waves' weight
+        // loads; at a higher issue priority they are not held behind loads that were merely
+        // ready to issue at the same time.
         __builtin_amdgcn_s_setprio(3);
-        // Lane 0: once a wait of this or any workgroup has run out (status set), no workgroup
-        // waits any more: the launch drains at once, every later y slab is NaN.  (A workgroup
-        // that stopped waiting runs ahead, and its arrivals can then interleave with another
-        // layer's, so a wait elsewhere might otherwise never see its count.)
-        bool late = false;
-        const auto wait_for = [&](uint32_t *c, uint32_t target) {
-            if (late) return;
-            uint32_t it = 0;
-            while (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-                if (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
-                    late = true;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-                if (++it >= spin_limit) {
-                    late = true;
-                    __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    record_wait_timeout(err, kWaitStack);
-                    break;
-                }
-            }
-        };
         for (uint32_t l = 0; l < L; ++l) {
-            if (l > 0) {  // B1
-                if (lane == 0) wait_for(ydone, DS * l);
-                lds_barrier();
-            }
+            const uint32_t t = tag_of(l);
+            const bool last = l + 1 == L;
             lds_barrier();  // B2: the gate/up parts, wave order
             float gs = 0.f, us = 0.f;
             for (uint32_t v = 0; v < W; ++v) {
@@ -1646,19 +1648,16 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
                 gs *= rs;
                 us *= rs;
             }
-            __hip_atomic_store(&h[g * kRowTile + lane], gelu_tanh(gs) * us, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            acknowledged();  // the h stores are acknowledged before the arrival is counted
-            if (lane == 0) {
-                __hip_atomic_fetch_add(&ready[kq * kCtrStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                wait_for(&ready[kq * kCtrStride], DS * (l + 1));
-            }
-            lds_barrier();  // B3: h's column part kq is complete
+            const float hv = gelu_tanh(gs) * us;
+            store_tagged(&htag[g * kRowTile + lane], hv, t);
+            if (last) h[g * kRowTile + lane] = hv;  // the caller's h: the last layer's
+            lds_barrier();  // B3: the parts have been read
             lds_barrier();  // B4: the down parts, wave order
             float r0 = 0.f;
             for (uint32_t v = 0; v < W; ++v) r0 += lds_part[v][0][lane];
             float *dst = partial + (size_t(dslab) * KQ + kq) * 64;
             __hip_atomic_store(&dst[lane], r0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            acknowledged();
+            acknowledged();  // the part is at the coherent level before it is counted
             uint32_t prev = 0;
             if (lane == 0)
                 prev = __hip_atomic_fetch_add(&arrive[dslab * kCtrStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1678,23 +1677,23 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
                         if (q0 + j < KQ) sum += v[j];
                 }
                 const bool bad = __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
-                __hip_atomic_store(&y[dslab * kRowTile + lane], bad ? __builtin_nanf("") : sum, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-                acknowledged();  // y_l's slab is written before it is counted
-                if (lane == 0) __hip_atomic_fetch_add(ydone, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const float yv = bad ? __builtin_nanf("") : sum;
+                if (last) y[dslab * kRowTile + lane] = yv;
+                else store_tagged(&ytag[dslab * kRowTile + lane], yv, t);
             }
-            if (l + 1 < L) lds_barrier();  // B5: the hand-off is done; the next layer's loads may go
+            if (!last) lds_barrier();  // B5: the hand-off is done; the next layer's loads may go
         }
-        // the last workgroup out clears the counters for the next launch (nothing polls them then)
+        // the last workgroup out clears the counters and advances the epoch for the next launch
+        // (nothing reads them any more in this one); this wave's stores and increments are
+        // performed before its exit is counted, so none can land after the clear
+        acknowledged();
         if (lane == 0) {
             const uint32_t done = __hip_atomic_fetch_add(exits, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (done == NG - 1) {
-                __hip_atomic_store(ydone, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 __hip_atomic_store(status, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                for (uint32_t k = 0; k < KQ; ++k)
-                    __hip_atomic_store(&ready[k * kCtrStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 for (uint32_t s = 0; s < DS; ++s)
                     __hip_atomic_store(&arrive[s * kCtrStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(epoch, E + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 __hip_atomic_store(exits, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
@@ -1732,22 +1731,38 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
                                                      16, vo, base + uint32_t(i) * 1024, 0, 0);
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
     };
+    // Re-reads this lane's 4 tagged words at p until the whole wave holds tag `want` (bounded;
+    // see Progress above).  v holds a first read already issued.
+    const auto settle = [&](const uint64_t *p, uint64_t (&v)[4], uint32_t want) {
+        uint32_t it = 0;
+        for (;;) {
+            const bool ok = tagged_tag(v[0]) == want && tagged_tag(v[1]) == want && tagged_tag(v[2]) == want &&
+                            tagged_tag(v[3]) == want;
+            if (__all(ok)) return;
+            if (__builtin_amdgcn_readfirstlane(__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)))
+                return;  // a wait elsewhere ran out: no more waiting
+            __builtin_amdgcn_s_sleep(1);
+            if (++it >= spin_limit) {
+                if (lane == 0) {
+                    __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    record_wait_timeout(err, kWaitStack);
+                }
+                return;
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k] = load_tagged(p + k);
+        }
+    };
     // One layer, per down type: the type branch encloses the whole layer, so that no value
-    // crosses from one layer to the next.  The layer's gate weights arrive in LDS during layer
-    // l-1's down phase (requested right after this wave's h loads, so they stream while the
-    // down dot products run); its up weights are requested first in the layer, before the
-    // wait for y_{l-1}, once this workgroup's hand-off of layer l-1 is done (B5) while other
-    // workgroups still finish that layer.  Requested at B4 instead, right after the down dot
-    // products, the loads sat ahead of the control wave's part store in the CU's memory
-    // pipeline and its acknowledgement took ~8 us (31.3 against 27.8 us per layer, with both
-    // halves loaded then).  Requested at the end of the previous iteration, register-held
-    // weights would be live across the loop's back edge, and the compiler spilled them.
+    // crosses from one layer to the next.  Register-held weights requested at the end of the
+    // previous iteration would be live across the loop's back edge, and the compiler spilled
+    // them: the up weights are requested first in the layer instead.
     const auto layer = [&](uint32_t l, auto tag) {
         constexpr bool q6 = decltype(tag)::value == Q6_K;
         const uint8_t *wd = layers.wd[l];
+        const uint32_t t = tag_of(l);
         if (l > 0) lds_barrier();  // B5: this workgroup's hand-off of layer l-1 is done
         load_up(l);
-        if (l > 0) lds_barrier();  // B1: y_{l-1} is complete
         u32x4 c[q6 ? kQ6Chunks : kQ4Chunks];
         uint32_t m6[q6 ? 64 : 1];
         uint32_t dbits = 0;
@@ -1758,11 +1773,13 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
             if (l == 0) {
                 xv = reinterpret_cast<const float4 *>(x0 + size_t(wave) * kQK)[lane];
             } else {
-                const float *xp = y + size_t(wave) * kQK + 4 * lane;
-                xv = float4{__hip_atomic_load(xp + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                            __hip_atomic_load(xp + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                            __hip_atomic_load(xp + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                            __hip_atomic_load(xp + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)};
+                // x_l = y_{l-1}: its tagged words, read behind the up weights
+                const uint64_t *xp = ytag + size_t(wave) * kQK + 4 * lane;
+                uint64_t xr[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) xr[k] = load_tagged(xp + k);
+                settle(xp, xr, t - 1u);
+                xv = float4{tagged_value(xr[0]), tagged_value(xr[1]), tagged_value(xr[2]), tagged_value(xr[3])};
             }
             float4 wv{1.f, 1.f, 1.f, 1.f};
             if constexpr (NORM) wv = reinterpret_cast<const float4 *>(layers.normw[l] + size_t(wave) * kQK)[lane];
@@ -1810,17 +1827,17 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
         {
             // ---- this wave's down part over h's column part kq ----
             const uint32_t lane = opaque_lane();
-            const float *hb = h + size_t(b) * kQK + 4 * lane;
-            // The h loads and the next layer's gate DMA in one block, which waits for the h loads
-            // only: the DMA streams while this layer's down dot products run.  The compiler does
-            // not see the DMA instructions; had it issued them, its first LDS access after them
-            // (the h values stored below) would wait for all of them, as it cannot tell that they
-            // write other LDS.  Vector memory operations complete in order, so operations the
-            // compiler does not count only make its own later waits stricter; the gate slot is
-            // read after an explicit wait for everything.  After the last layer the same block
-            // runs with a buffer range of 0: the DMA reads are out of range, which reads no
-            // memory and writes zeros to the slot (one block, one wait count, no branch).
-            u32x4 hraw;
+            const uint64_t *hp = htag + size_t(b) * kQK + 4 * lane;
+            // The first read of h's tagged words and the next layer's gate DMA in one block,
+            // which waits for the h loads only: the DMA streams while this layer's down dot
+            // products run.  The compiler does not see the DMA instructions; had it issued them,
+            // its first LDS access after them (the h values stored below) would wait for all of
+            // them, as it cannot tell that they write other LDS.  Vector memory operations
+            // complete in order, so operations the compiler does not count only make its own
+            // later waits stricter; the gate slot is read after an explicit wait for everything.
+            // After the last layer the same block runs with a buffer range of 0: the DMA reads are
+            // out of range, which reads no memory and writes zeros to the slot.
+            u32x4 h0, h1;
             {
                 const bool next = l + 1 < L;
                 const uint64_t gb = reinterpret_cast<uint64_t>(layers.wg[next ? l + 1 : l]);
@@ -1835,22 +1852,25 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
                 uint32_t st;
 #define NS_GATE_DMA "s_nop 0\n\tbuffer_load_dwordx4 %[vo], %[rs], %[st] offen lds\n\t"
 #define NS_GATE_NEXT "s_add_u32 m0, m0, 0x400\n\ts_add_u32 %[st], %[st], 0x400\n\t"
-                asm volatile("global_load_dwordx4 %[hv], %[ha], off sc1\n\t"
+                asm volatile("global_load_dwordx4 %[h0], %[ha], off sc1\n\t"
+                             "global_load_dwordx4 %[h1], %[ha], off offset:16 sc1\n\t"
                              "s_mov_b32 m0, %[lds]\n\t"
                              "s_mov_b32 %[st], %[so]\n\t" NS_GATE_DMA NS_GATE_NEXT NS_GATE_DMA NS_GATE_NEXT NS_GATE_DMA
                                  NS_GATE_NEXT NS_GATE_DMA NS_GATE_NEXT NS_GATE_DMA NS_GATE_NEXT NS_GATE_DMA NS_GATE_NEXT
                                      NS_GATE_DMA NS_GATE_NEXT NS_GATE_DMA NS_GATE_NEXT NS_GATE_DMA
                              "s_waitcnt vmcnt(9)"
-                             : [hv] "=&v"(hraw), [st] "=&s"(st)
-                             : [ha] "v"(hb), [rs] "s"(rs), [so] "s"(so), [lds] "s"(lds), [vo] "v"(vo)
+                             : [h0] "=&v"(h0), [h1] "=&v"(h1), [st] "=&s"(st)
+                             : [ha] "v"(hp), [rs] "s"(rs), [so] "s"(so), [lds] "s"(lds), [vo] "v"(vo)
                              : "memory", "m0", "scc");
 #undef NS_GATE_DMA
 #undef NS_GATE_NEXT
             }
-            // lanes go through a by-value argument: clang's __builtin_bit_cast applied to a lane
-            // of an ext-vector reads lane 0 whatever the lane
-            const auto as_f = [](uint32_t v) { return __builtin_bit_cast(float, v); };
-            const float4 hv{as_f(hraw.x), as_f(hraw.y), as_f(hraw.z), as_f(hraw.w)};
+            // lanes go through by-value arguments: clang's __builtin_bit_cast applied to a lane of
+            // an ext-vector reads lane 0 whatever the lane
+            const auto word = [](uint32_t lo, uint32_t hi) { return uint64_t(lo) | (uint64_t(hi) << 32); };
+            uint64_t hr[4] = {word(h0.x, h0.y), word(h0.z, h0.w), word(h1.x, h1.y), word(h1.z, h1.w)};
+            settle(hp, hr, t);
+            const float4 hv{tagged_value(hr[0]), tagged_value(hr[1]), tagged_value(hr[2]), tagged_value(hr[3])};
             uint32_t lane_b = lane;
             asm volatile("" : "+v"(lane_b));
             reinterpret_cast<float4 *>(xw)[lane_b] = hv;
@@ -1876,7 +1896,6 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
         else layer(l, DTag<Q4_K>{});
     }
 }
-
 }  // namespace
 
 void gemv_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, bool pair, const Tuning &t,
@@ -2011,19 +2030,20 @@ bool stack_decode_supported(int layout, bool norm, uint32_t cols, uint32_t ffn) 
 
 void stack_decode_workspace_need(uint32_t cols, uint32_t ffn, size_t *partial_floats, size_t *counters) {
     const uint32_t KQ = (ffn / kQK) / (cols / kQK), DS = cols / kRowTile;
-    *partial_floats = size_t(DS) * KQ * 64;         // the down projection's column parts
-    *counters = size_t(kCtrStride) * (2 + KQ + DS);  // ydone; status, exits; ready[KQ]; arrive[DS]
+    *partial_floats = size_t(DS) * KQ * 64;  // the down projection's column parts
+    *counters = size_t(kCtrStride) * (1 + DS);  // status, exits; arrive[DS]
 }
 
 hipError_t launch_stack_decode(uint32_t n_layers, const uint8_t *const *wg, const uint8_t *const *wu,
                                const uint8_t *const *wd, const int *down_types, const float *x,
                                const float *const *normw, float eps, float *h, float *y, uint32_t cols, uint32_t ffn,
-                               const Workspace &ws, hipStream_t stream) {
+                               const Workspace &ws, const StackBuffers &sb, hipStream_t stream) {
     const bool norm = normw != nullptr;
     if (n_layers == 0 || !stack_decode_supported(CDNA4, norm, cols, ffn)) return hipErrorInvalidValue;
     size_t pf = 0, nc = 0;
     stack_decode_workspace_need(cols, ffn, &pf, &nc);
-    if (ws.partial_floats < pf || ws.counter_count < nc) return hipErrorInvalidValue;
+    if (ws.partial_floats < pf || ws.counter_count < nc || !sb.epoch || sb.cols < cols || sb.ffn < ffn)
+        return hipErrorInvalidValue;
     // 2^22 polls, each an L2 round trip plus s_sleep 1: seconds
     const uint32_t spin = ws.tune.block_spin > 0 ? uint32_t(ws.tune.block_spin) : 1u << 22;
     const dim3 g(ffn / kRowTile), blk((cols / kQK + 1) * 64);
@@ -2040,8 +2060,12 @@ hipError_t launch_stack_decode(uint32_t n_layers, const uint8_t *const *wg, cons
             if (down_types[l0 + l] == Q6_K) t.q6_down |= uint64_t(1) << l;
         }
         const float *xin = l0 == 0 ? x : y;
-        if (norm) stack_decode_kernel<true><<<g, blk, 0, stream>>>(t, L, xin, eps, h, y, cols, ffn, ws.partial, ws.counters, spin, ws.err);
-        else stack_decode_kernel<false><<<g, blk, 0, stream>>>(t, L, xin, eps, h, y, cols, ffn, ws.partial, ws.counters, spin, ws.err);
+        const auto run = [&](auto kernel) {
+            kernel<<<g, blk, 0, stream>>>(t, L, xin, eps, h, y, cols, ffn, ws.partial, ws.counters, sb.epoch, sb.htag,
+                                          sb.ytag, spin, ws.err);
+        };
+        if (norm) run(&stack_decode_kernel<true>);
+        else run(&stack_decode_kernel<false>);
         if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     }
     return hipSuccess;

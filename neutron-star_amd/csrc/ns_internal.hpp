@@ -102,12 +102,20 @@ hipError_t launch_block_decode(int down_type, const uint8_t *wg, const uint8_t *
 // place), CDNA4 layout, shapes with (ffn/256) a multiple of (cols/256) < 16.  normw non-null:
 // layer l folds the RMSNorm of its input (weight normw[l], eps) into its gate/up dot products.
 // Host arrays of device pointers; down_types[l] is Q4_K or Q6_K.
+// Device buffers of that launch that outlive a call, owned by the context: the epoch (a counter
+// each launch advances, so that values an earlier launch left carry no current tag; starts at
+// 1) and the tagged copies of h [ffn] and y [cols] (64-bit words, zero at allocation).
+struct StackBuffers {
+    uint32_t *epoch = nullptr;
+    uint64_t *htag = nullptr, *ytag = nullptr;
+    uint32_t cols = 0, ffn = 0;
+};
 bool stack_decode_supported(int layout, bool norm, uint32_t cols, uint32_t ffn);
 void stack_decode_workspace_need(uint32_t cols, uint32_t ffn, size_t *partial_floats, size_t *counters);
 hipError_t launch_stack_decode(uint32_t n_layers, const uint8_t *const *wg, const uint8_t *const *wu,
                                const uint8_t *const *wd, const int *down_types, const float *x,
                                const float *const *normw, float eps, float *h, float *y, uint32_t cols, uint32_t ffn,
-                               const Workspace &ws, hipStream_t stream);
+                               const Workspace &ws, const StackBuffers &sb, hipStream_t stream);
 
 // Batch 1-4 on the matrix cores (ns_gemv_mfma.hip), CDNA4 layout; launch_gemv_mt routes there
 // when gemv_mfma_eligible.
