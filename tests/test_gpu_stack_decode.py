@@ -14,7 +14,9 @@ consecutive layers (the engine's per-layer decode FFN, metal_engine.mm:563-573, 
   * y aliasing x, repeated launches (the counters reset), HIP graph replays;
   * the bounded waits, forced down to one poll from the host: y is NaN, the context's status
     reports NS_ERR_TIMEOUT once, and the next launch is exact again;
-  * the wait-free context runs one block per layer: the same bits.
+  * the wait-free context runs one block per layer: the same bits;
+  * launches of different lengths and shapes alternating on one context (the epoch), and a shape
+    that grows the context's tagged buffers.
 """
 import numpy as np
 import pytest
@@ -256,3 +258,34 @@ def test_stack_argument_errors(ctx):
         ctx.ffn_stack_decode([], [], [], [], N.CDNA4, D, F, x, h, x)
     with pytest.raises(N.NsError, match="type"):
         ctx.ffn_stack_decode(wg, wu, wd, [N.Q4_K, 3], N.CDNA4, D, F, x, h, x, norm_weights=nws)
+
+
+def test_stack_epochs_across_launch_lengths(ctx):
+    """Launches of different lengths and shapes alternate on one context (the epoch advances per
+    launch, the tagged buffers are shared): every launch equals its per-layer blocks, so no
+    launch reads a value an earlier one left behind."""
+    big = make_stack(0xE4, 6, 3840, 15360, norm=True)
+    small = make_stack(0xE6, 3, 1024, 4096, norm=True)
+    xb = torch.from_numpy(N.synth_normal_f32(0xE5, 3840)).cuda()
+    xs = torch.from_numpy(N.synth_normal_f32(0xE7, 1024)).cuda()
+    for st, D, F, x, Ls in ((big, 3840, 15360, xb, (1, 6, 2)), (small, 1024, 4096, xs, (3, 1)),
+                            (big, 3840, 15360, xb, (6, 1))):
+        for L in Ls:
+            sub = tuple(v[:L] if isinstance(v, list) else v for v in st)
+            _, y1 = run_stack(ctx, sub, D, F, x)
+            _, y2 = run_blocks(ctx, sub, D, F, x)
+            assert np.array_equal(bits(y1), bits(y2)), (D, L)
+    ctx.status()
+
+
+def test_stack_grows_its_tagged_buffers(ctx):
+    """A shape past the model's (16384 ffn rows: 256 workgroups, one per CU) grows the context's
+    tagged h buffer; the result equals the per-layer blocks."""
+    D, F, L = 2048, 16384, 3
+    st = make_stack(0xE8, L, D, F, norm=True)
+    x = torch.from_numpy(N.synth_normal_f32(0xE9, D)).cuda()
+    h1, y1 = run_stack(ctx, st, D, F, x)
+    h2, y2 = run_blocks(ctx, st, D, F, x)
+    ctx.status()
+    assert np.isfinite(y1.cpu().numpy()).all()
+    assert np.array_equal(bits(y1), bits(y2)) and np.array_equal(bits(h1), bits(h2))
