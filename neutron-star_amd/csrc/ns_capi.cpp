@@ -24,7 +24,8 @@ struct ns_ctx {
     // Device word the kernels OR a WaitBit into when a bounded cross-workgroup wait runs out
     // (ws.err points here); read and cleared by ns_ctx_status.
     uint32_t *err = nullptr;
-    // The multi-layer decode launch's epoch and tagged h / y (one allocation).
+    // The decode block's and the multi-layer decode launch's epoch and tagged h / y (one
+    // allocation).
     ns::StackBuffers stack;
     void *stack_mem = nullptr;
 };
@@ -522,9 +523,10 @@ extern "C" int ns_ffn_block_decode(ns_ctx *ctx, const void *wg, const void *wu, 
         size_t pf = 0, nc = 0;
         block_decode_workspace_need(cols, ffn, &pf, &nc);
         if (int rc = ensure_ws(ctx, pf, nc, s)) return rc;
+        if (int rc = ensure_stack(ctx, cols, ffn, s)) return rc;
         const hipError_t e = launch_block_decode(down_type, static_cast<const uint8_t *>(wg),
                                                  static_cast<const uint8_t *>(wu), static_cast<const uint8_t *>(wd), x,
-                                                 norm_weight, eps, h, y, cols, ffn, ctx->ws, s);
+                                                 norm_weight, eps, h, y, cols, ffn, ctx->ws, ctx->stack, s);
         return e == hipSuccess ? NS_OK : hip_fail(e, fn);
     }
     // two launches (mm:571-573): gate/up + GeGLU (with the norm when given), then down

@@ -89,6 +89,15 @@ void gemv_workspace_need(int type, int layout, uint32_t cols, uint32_t rows, boo
 hipError_t launch_gemv_mt(int type, int layout, const uint8_t *w, const uint8_t *up, const void *x, bool xh,
                           uint32_t batch, void *out, uint32_t cols, uint32_t rows, const Workspace &ws,
                           hipStream_t stream);
+// Device buffers of the one-launch decode block and the multi-layer decode launch that outlive
+// a call, owned by the context: the epoch (a counter each launch advances, so that values an
+// earlier launch left carry no current tag; starts at 1) and the tagged copies of h [ffn] and
+// y [cols] (64-bit words, zero at allocation).
+struct StackBuffers {
+    uint32_t *epoch = nullptr;
+    uint64_t *htag = nullptr, *ytag = nullptr;
+    uint32_t cols = 0, ffn = 0;
+};
 // The decode FFN block in one launch (gate/up + GeGLU into h, then down into y), CDNA4
 // layout, shapes with (ffn/256) a multiple of (cols/256) <= 16.  normw non-null folds the
 // RMSNorm of x (weight normw, eps) into the gate/up dot products.  y may alias x; h may not.
@@ -96,20 +105,12 @@ bool block_decode_supported(int layout, int down_type, bool norm, uint32_t cols,
 void block_decode_workspace_need(uint32_t cols, uint32_t ffn, size_t *partial_floats, size_t *counters);
 hipError_t launch_block_decode(int down_type, const uint8_t *wg, const uint8_t *wu, const uint8_t *wd, const float *x,
                                const float *normw, float eps, float *h, float *y, uint32_t cols, uint32_t ffn,
-                               const Workspace &ws, hipStream_t stream);
+                               const Workspace &ws, const StackBuffers &sb, hipStream_t stream);
 
 // The decode FFN blocks of n_layers consecutive layers in one launch (x_{l+1} = y_l, y updated in
 // place), CDNA4 layout, shapes with (ffn/256) a multiple of (cols/256) < 16.  normw non-null:
 // layer l folds the RMSNorm of its input (weight normw[l], eps) into its gate/up dot products.
 // Host arrays of device pointers; down_types[l] is Q4_K or Q6_K.
-// Device buffers of that launch that outlive a call, owned by the context: the epoch (a counter
-// each launch advances, so that values an earlier launch left carry no current tag; starts at
-// 1) and the tagged copies of h [ffn] and y [cols] (64-bit words, zero at allocation).
-struct StackBuffers {
-    uint32_t *epoch = nullptr;
-    uint64_t *htag = nullptr, *ytag = nullptr;
-    uint32_t cols = 0, ffn = 0;
-};
 bool stack_decode_supported(int layout, bool norm, uint32_t cols, uint32_t ffn);
 void stack_decode_workspace_need(uint32_t cols, uint32_t ffn, size_t *partial_floats, size_t *counters);
 hipError_t launch_stack_decode(uint32_t n_layers, const uint8_t *const *wg, const uint8_t *const *wu,
