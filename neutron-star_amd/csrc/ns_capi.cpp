@@ -110,7 +110,7 @@ int ensure_stack(ns_ctx *ctx, uint32_t cols, uint32_t ffn, hipStream_t s) {
     hipError_t e = hipSetDevice(ctx->device);
     if (e != hipSuccess) return hip_fail(e, "decode buffer growth");
     const uint32_t c = std::max(cols, sb.cols), f = std::max(ffn, sb.ffn);
-    const size_t bytes = 256 + (size_t(f) + c) * sizeof(uint64_t);
+    const size_t bytes = 256 + (2 * size_t(f) + c) * sizeof(uint64_t);
     void *p = nullptr;
     e = hipMalloc(&p, bytes);
     if (e == hipSuccess) e = hipMemset(p, 0, bytes);
@@ -125,6 +125,7 @@ int ensure_stack(ns_ctx *ctx, uint32_t cols, uint32_t ffn, hipStream_t s) {
     sb.epoch = static_cast<uint32_t *>(p);
     sb.htag = reinterpret_cast<uint64_t *>(static_cast<char *>(p) + 256);
     sb.ytag = sb.htag + f;
+    sb.ptag = sb.ytag + c;
     sb.cols = c;
     sb.ffn = f;
     return NS_OK;

@@ -1318,8 +1318,10 @@ uint32_t mt_tokens(uint32_t batch, bool xh) { return xh && batch <= 2 ? 2u : 4u;
 //      their gate/up slabs;
 //   3. each wave reads its 256 values of h (from the DS gate/up slabs of part kq, workgroups
 //      kq*DS .. kq*DS + DS-1) as tagged words and re-reads until every tag is current, then
-//      finishes as the decode GEMV's k-workgroups-per-slab plan does: the KQ parts of one slab
-//      added in part order by the last to arrive.
+//      forms its part of the down projection; wave 0 stores the workgroup's part as tagged
+//      words, and the slab's reducer, the workgroup of part kq = 0, re-reads the other KQ-1
+//      parts until they are current and adds them in part order (the order of the decode
+//      GEMV's k-workgroups-per-slab plan).
 // The tag is the launch's epoch * 64 + 1.  The epoch is a context-owned counter that the
 // launch's last slab advances (the multi-layer launch below advances the same counter), so
 // words left by an earlier launch carry no current tag; with the tags no counter has to be
@@ -1350,6 +1352,46 @@ __device__ __forceinline__ uint64_t load_tagged(const uint64_t *p) {
 __device__ __forceinline__ float tagged_value(uint64_t w) { return __builtin_bit_cast(float, uint32_t(w)); }
 __device__ __forceinline__ uint32_t tagged_tag(uint64_t w) { return uint32_t(w >> 32); }
 
+// A slab's reducer: the KQ column parts of this lane's output row ([KQ][64] tagged words at
+// parts), added in part order from 0, with its own part `own` taken from `mine`; the others
+// are read 16 at a time and re-read until their tags are `tag` (bounded by spin_limit polls;
+// once status is set nothing waits, and a wait that runs out sets status and records `bit`).
+// The order of the sum is that of the last-arriver hand-off it replaces, so the result is the
+// same bit for bit.
+__device__ __forceinline__ float reduce_tagged_parts(const uint64_t *parts, uint32_t KQ, uint32_t own, float mine,
+                                                     uint32_t lane, uint32_t tag, uint32_t spin_limit,
+                                                     uint32_t *status, uint32_t *err, uint32_t bit) {
+    float sum = 0.f;
+    for (uint32_t q0 = 0; q0 < KQ; q0 += 16) {
+        uint64_t v[16];
+#pragma unroll
+        for (uint32_t j = 0; j < 16; ++j) v[j] = load_tagged(parts + __builtin_elementwise_min(q0 + j, KQ - 1) * 64 + lane);
+        for (uint32_t it = 0;;) {
+            bool ok = true;
+#pragma unroll
+            for (uint32_t j = 0; j < 16; ++j)
+                if (q0 + j < KQ && q0 + j != own) ok = ok && tagged_tag(v[j]) == tag;
+            if (__all(ok)) break;
+            if (__builtin_amdgcn_readfirstlane(__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) break;
+            __builtin_amdgcn_s_sleep(1);
+            if (++it >= spin_limit) {
+                if (lane == 0) {
+                    __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    record_wait_timeout(err, bit);
+                }
+                break;
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < 16; ++j)
+                v[j] = load_tagged(parts + __builtin_elementwise_min(q0 + j, KQ - 1) * 64 + lane);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < 16; ++j)
+            if (q0 + j < KQ) sum += q0 + j == own ? mine : tagged_value(v[j]);
+    }
+    return sum;
+}
+
 // signal fences keep the compiler from moving memory operations across the barrier; the
 // barrier itself does not wait for this wave's global loads in flight
 __device__ __forceinline__ void lds_barrier() {
@@ -1365,8 +1407,8 @@ template <int DTYPE, bool NORM>
 __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) void block_decode_kernel(
     const uint8_t *__restrict__ wg, const uint8_t *__restrict__ wu, const uint8_t *__restrict__ wd,
     const float *__restrict__ x, const float *__restrict__ normw, float eps, float *__restrict__ h,
-    float *__restrict__ y, uint32_t D, uint32_t F, float *__restrict__ partial, uint32_t *__restrict__ ctr,
-    uint32_t spin_limit, uint32_t *__restrict__ err, uint32_t *__restrict__ epoch, uint64_t *__restrict__ htag) {
+    float *__restrict__ y, uint32_t D, uint32_t F, uint32_t *__restrict__ ctr, uint32_t spin_limit,
+    uint32_t *__restrict__ err, uint32_t *__restrict__ epoch, uint64_t *__restrict__ htag, uint64_t *__restrict__ ptag) {
     __shared__ __attribute__((aligned(16))) float lds_x[kBlockMaxW * kQK];
     __shared__ float lds_part[kBlockMaxW][2][64];
     __shared__ float lds_sum[kBlockMaxW];
@@ -1374,8 +1416,8 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t nbg = D / kQK, nbd = F / kQK, KQ = nbd / nbg, DS = D / kRowTile, W = nbg;
     const uint32_t g = blockIdx.x, kq = g / DS, dslab = g - kq * DS;
-    // ctr: slabs_done, status, then arrive[DS], each on a line of its own
-    uint32_t *slabs_done = ctr, *status = ctr + 1, *arrive = ctr + kCtrStride;
+    // ctr: slabs_done, status
+    uint32_t *slabs_done = ctr, *status = ctr + 1;
     float *xw = lds_x + wave * kQK;  // this wave's 256 inputs
     // the launch's tag: every wave reads the epoch before the last slab can advance it
     const uint32_t E = __builtin_amdgcn_readfirstlane(__hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
@@ -1501,35 +1543,16 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
     if (wave == 0) {
         float r0 = 0.f;
         for (uint32_t v = 0; v < W; ++v) r0 += lds_part[v][0][lane];
-        float *dst = partial + (size_t(dslab) * KQ + kq) * 64;
-        __hip_atomic_store(&dst[lane], r0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_s_waitcnt(0);
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        uint32_t prev = 0;
-        if (lane == 0)
-            prev = __hip_atomic_fetch_add(&arrive[dslab * kCtrStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        prev = __builtin_amdgcn_readfirstlane(__shfl(prev, 0));
-        if (prev == KQ - 1) {
-            // the column parts of the slab, loaded 16 at a time and added in part order
-            float sum = 0.f;
-            const float *src = partial + size_t(dslab) * KQ * 64;
-            for (uint32_t q0 = 0; q0 < KQ; q0 += 16) {
-                float v[16];
-#pragma unroll
-                for (uint32_t j = 0; j < 16; ++j)
-                    v[j] = __hip_atomic_load(&src[__builtin_elementwise_min(q0 + j, KQ - 1) * 64 + lane],
-                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-                for (uint32_t j = 0; j < 16; ++j)
-                    if (q0 + j < KQ) sum += v[j];
-            }
+        store_tagged(&ptag[(size_t(dslab) * KQ + kq) * 64 + lane], r0, tg);
+        if (kq == 0) {
+            // the slab's reducer: its KQ column parts added in part order
+            const float sum = reduce_tagged_parts(ptag + size_t(dslab) * KQ * 64, KQ, 0, r0, lane, tg, spin_limit,
+                                                  status, err, kWaitBlock);
             // a part that stopped waiting read h too early: the slab is not a result
             const bool late = __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
             y[dslab * kRowTile + lane] = late ? __builtin_nanf("") : sum;
             if (lane == 0) {
-                __hip_atomic_store(&arrive[dslab * kCtrStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                // every workgroup has arrived once the last slab is done: nothing reads
+                // every workgroup's part has been read once the last slab is done: nothing reads
                 // status or the epoch any more in this launch
                 const uint32_t done = __hip_atomic_fetch_add(slabs_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 if (done == DS - 1) {
@@ -1562,7 +1585,8 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
 // find the values there in the common case.  The epoch lives in a buffer of its own that the
 // launch's last workgroup advances, so a word left by an earlier launch (or zeroed at
 // allocation: tag 0, the epoch starts at 1) never carries a current tag, also across graph
-// replays.  Only y's column parts still meet by the last-arriver hand-off (arrive[dslab]).
+// replays.  y's column parts are tagged words too: each slab's reducer (the workgroup of
+// part 0) re-reads the others until they are current and adds them in part order.
 //
 // Per layer l, four workgroup barriers:
 //   B5  (l > 0) the control wave has handed off layer l-1: the compute waves request layer
@@ -1573,9 +1597,9 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
 //   B3  the control wave's reads of the parts are done; the compute waves read their 256
 //       values of h (tags of layer l), request the next layer's gate weights into LDS and form
 //       their down parts;
-//   B4  the down parts are in LDS: the control wave stores the workgroup's part, counts it on
-//       arrive[dslab] and, as the KQ*(l+1)-th arrival, adds the KQ parts in part order into
-//       y_l (tagged; the caller's y, plainly, after the last layer); then B5.
+//   B4  the down parts are in LDS: the control wave stores the workgroup's part tagged; in the
+//       slab's reducer (kq = 0) it then adds the KQ parts in part order into y_l (tagged; the
+//       caller's y, plainly, after the last layer); then B5.
 // The gate DMA and the up loads stay out of the control wave's way: the DMA is requested
 // after the compute waves' h loads and streams during the down dot products; the up loads
 // wait for B5, since requested at B4 the loads sat ahead of the control wave's part store in
@@ -1612,8 +1636,8 @@ struct StackLayers {
 template <bool NORM>
 __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) void stack_decode_kernel(
     const StackLayers layers, uint32_t L, const float *x0, float eps, float *__restrict__ h, float *y, uint32_t D,
-    uint32_t F, float *__restrict__ partial, uint32_t *__restrict__ ctr, uint32_t *__restrict__ epoch,
-    uint64_t *__restrict__ htag, uint64_t *__restrict__ ytag, uint32_t spin_limit, uint32_t *__restrict__ err) {
+    uint32_t F, uint32_t *__restrict__ ctr, uint32_t *__restrict__ epoch, uint64_t *__restrict__ htag,
+    uint64_t *__restrict__ ytag, uint64_t *__restrict__ ptag, uint32_t spin_limit, uint32_t *__restrict__ err) {
     // each compute wave's gate super-block of the next layer, DMA'd from HBM (9 KiB a wave)
     __shared__ __attribute__((aligned(16))) u32x4 lds_gate[kBlockMaxW - 1][kQ4Chunks][64];
     __shared__ __attribute__((aligned(16))) float lds_x[(kBlockMaxW - 1) * kQK];
@@ -1623,8 +1647,8 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t nbg = D / kQK, nbd = F / kQK, KQ = nbd / nbg, DS = D / kRowTile, W = nbg, NG = DS * KQ;
     const uint32_t g = blockIdx.x, kq = g / DS, dslab = g - kq * DS;
-    // ctr: status, exits; then arrive[DS], each on a line of its own
-    uint32_t *status = ctr, *exits = ctr + 1, *arrive = ctr + kCtrStride;
+    // ctr: status, exits
+    uint32_t *status = ctr, *exits = ctr + 1;
     // the launch's epoch: read by every wave before any workgroup can have exited (the last one
     // out advances it)
     const uint32_t E = __builtin_amdgcn_readfirstlane(__hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
@@ -1668,27 +1692,11 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
             lds_barrier();  // B4: the down parts, wave order
             float r0 = 0.f;
             for (uint32_t v = 0; v < W; ++v) r0 += lds_part[v][0][lane];
-            float *dst = partial + (size_t(dslab) * KQ + kq) * 64;
-            __hip_atomic_store(&dst[lane], r0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            acknowledged();  // the part is at the coherent level before it is counted
-            uint32_t prev = 0;
-            if (lane == 0)
-                prev = __hip_atomic_fetch_add(&arrive[dslab * kCtrStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            prev = __builtin_amdgcn_readfirstlane(__shfl(prev, 0));
-            if (prev == KQ * (l + 1) - 1) {
-                // the column parts of the slab, loaded 16 at a time and added in part order
-                float sum = 0.f;
-                const float *src = partial + size_t(dslab) * KQ * 64;
-                for (uint32_t q0 = 0; q0 < KQ; q0 += 16) {
-                    float v[16];
-#pragma unroll
-                    for (uint32_t j = 0; j < 16; ++j)
-                        v[j] = __hip_atomic_load(&src[__builtin_elementwise_min(q0 + j, KQ - 1) * 64 + lane],
-                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-                    for (uint32_t j = 0; j < 16; ++j)
-                        if (q0 + j < KQ) sum += v[j];
-                }
+            store_tagged(&ptag[(size_t(dslab) * KQ + kq) * 64 + lane], r0, t);
+            if (kq == 0) {
+                // the slab's reducer: its KQ column parts added in part order
+                const float sum = reduce_tagged_parts(ptag + size_t(dslab) * KQ * 64, KQ, 0, r0, lane, t, spin_limit,
+                                                      status, err, kWaitStack);
                 const bool bad = __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
                 const float yv = bad ? __builtin_nanf("") : sum;
                 if (last) y[dslab * kRowTile + lane] = yv;
@@ -1704,8 +1712,6 @@ __global__ __launch_bounds__(kBlockMaxW * 64) __attribute__((amdgpu_waves_per_eu
             const uint32_t done = __hip_atomic_fetch_add(exits, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (done == NG - 1) {
                 __hip_atomic_store(status, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                for (uint32_t s = 0; s < DS; ++s)
-                    __hip_atomic_store(&arrive[s * kCtrStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 __hip_atomic_store(epoch, E + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 __hip_atomic_store(exits, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
@@ -1985,9 +1991,10 @@ bool block_decode_supported(int layout, int down_type, bool norm, uint32_t cols,
 }
 
 void block_decode_workspace_need(uint32_t cols, uint32_t ffn, size_t *partial_floats, size_t *counters) {
-    const uint32_t KQ = (ffn / kQK) / (cols / kQK), DS = cols / kRowTile;
-    *partial_floats = size_t(DS) * KQ * 64;         // the down projection's column parts
-    *counters = size_t(kCtrStride) * (1 + DS);  // slabs_done, status; arrive[DS]
+    (void)cols;
+    (void)ffn;
+    *partial_floats = 0;     // the column parts are tagged words in the context's buffers
+    *counters = kCtrStride;  // slabs_done, status
 }
 
 hipError_t launch_block_decode(int down_type, const uint8_t *wg, const uint8_t *wu, const uint8_t *wd, const float *x,
@@ -1996,13 +2003,13 @@ hipError_t launch_block_decode(int down_type, const uint8_t *wg, const uint8_t *
     if (!block_decode_supported(CDNA4, down_type, normw != nullptr, cols, ffn)) return hipErrorInvalidValue;
     size_t pf = 0, nc = 0;
     block_decode_workspace_need(cols, ffn, &pf, &nc);
-    if (ws.partial_floats < pf || ws.counter_count < nc || !sb.epoch || sb.ffn < ffn) return hipErrorInvalidValue;
+    if (ws.counter_count < nc || !sb.epoch || sb.ffn < ffn) return hipErrorInvalidValue;
     // 2^22 polls, each an L2 round trip plus s_sleep 1: seconds
     const uint32_t spin = ws.tune.block_spin > 0 ? uint32_t(ws.tune.block_spin) : 1u << 22;
     const dim3 g(ffn / kRowTile), blk((cols / kQK) * 64);
     const auto args = [&](auto kernel) {
-        kernel<<<g, blk, 0, stream>>>(wg, wu, wd, x, normw, eps, h, y, cols, ffn, ws.partial, ws.counters, spin, ws.err,
-                                      sb.epoch, sb.htag);
+        kernel<<<g, blk, 0, stream>>>(wg, wu, wd, x, normw, eps, h, y, cols, ffn, ws.counters, spin, ws.err, sb.epoch,
+                                      sb.htag, sb.ptag);
     };
     if (down_type == Q4_K) {
         if (normw) args(block_kernel_of<Q4_K, true>());
@@ -2043,9 +2050,10 @@ bool stack_decode_supported(int layout, bool norm, uint32_t cols, uint32_t ffn) 
 }
 
 void stack_decode_workspace_need(uint32_t cols, uint32_t ffn, size_t *partial_floats, size_t *counters) {
-    const uint32_t KQ = (ffn / kQK) / (cols / kQK), DS = cols / kRowTile;
-    *partial_floats = size_t(DS) * KQ * 64;  // the down projection's column parts
-    *counters = size_t(kCtrStride) * (1 + DS);  // status, exits; arrive[DS]
+    (void)cols;
+    (void)ffn;
+    *partial_floats = 0;     // the column parts are tagged words in the context's buffers
+    *counters = kCtrStride;  // status, exits
 }
 
 hipError_t launch_stack_decode(uint32_t n_layers, const uint8_t *const *wg, const uint8_t *const *wu,
@@ -2056,8 +2064,7 @@ hipError_t launch_stack_decode(uint32_t n_layers, const uint8_t *const *wg, cons
     if (n_layers == 0 || !stack_decode_supported(CDNA4, norm, cols, ffn)) return hipErrorInvalidValue;
     size_t pf = 0, nc = 0;
     stack_decode_workspace_need(cols, ffn, &pf, &nc);
-    if (ws.partial_floats < pf || ws.counter_count < nc || !sb.epoch || sb.cols < cols || sb.ffn < ffn)
-        return hipErrorInvalidValue;
+    if (ws.counter_count < nc || !sb.epoch || sb.cols < cols || sb.ffn < ffn) return hipErrorInvalidValue;
     // 2^22 polls, each an L2 round trip plus s_sleep 1: seconds
     const uint32_t spin = ws.tune.block_spin > 0 ? uint32_t(ws.tune.block_spin) : 1u << 22;
     const dim3 g(ffn / kRowTile), blk((cols / kQK + 1) * 64);
@@ -2075,8 +2082,8 @@ hipError_t launch_stack_decode(uint32_t n_layers, const uint8_t *const *wg, cons
         }
         const float *xin = l0 == 0 ? x : y;
         const auto run = [&](auto kernel) {
-            kernel<<<g, blk, 0, stream>>>(t, L, xin, eps, h, y, cols, ffn, ws.partial, ws.counters, sb.epoch, sb.htag,
-                                          sb.ytag, spin, ws.err);
+            kernel<<<g, blk, 0, stream>>>(t, L, xin, eps, h, y, cols, ffn, ws.counters, sb.epoch, sb.htag, sb.ytag,
+                                          sb.ptag, spin, ws.err);
         };
         if (norm) run(&stack_decode_kernel<true>);
         else run(&stack_decode_kernel<false>);

@@ -92,10 +92,11 @@ hipError_t launch_gemv_mt(int type, int layout, const uint8_t *w, const uint8_t 
 // Device buffers of the one-launch decode block and the multi-layer decode launch that outlive
 // a call, owned by the context: the epoch (a counter each launch advances, so that values an
 // earlier launch left carry no current tag; starts at 1) and the tagged copies of h [ffn] and
-// y [cols] (64-bit words, zero at allocation).
+// y [cols], and the down projection's tagged column parts [ffn] (64-bit words, zero at
+// allocation).
 struct StackBuffers {
     uint32_t *epoch = nullptr;
-    uint64_t *htag = nullptr, *ytag = nullptr;
+    uint64_t *htag = nullptr, *ytag = nullptr, *ptag = nullptr;
     uint32_t cols = 0, ffn = 0;
 };
 // The decode FFN block in one launch (gate/up + GeGLU into h, then down into y), CDNA4
