@@ -559,8 +559,8 @@ class Bench:
         """The launch sequence the rocprofv3 --pmc passes read: every prefill GEMM instance at
         batch 1024 (gate/up pair, Q6_K and Q4_K down; FP32 then FP16 mode), the decode GEMVs
         (config 0's Q4_K, config 1's Q6_K down, the gate/up pair) and the batch-4 kernels (the
-        lm-head, the gate/up pair, the Q6_K down) and config 2's decode block in one launch,
-        --steps launches each, then three copies of a
+        lm-head, the gate/up pair, the Q6_K down), config 2's decode block in one launch and 8 of
+        config 4's decode layers in one launch, --steps launches each, then three copies of a
         256 MiB buffer, the copy of known size that scales FETCH_SIZE and WRITE_SIZE.  Weights
         rotate over two copies so a launch cannot find the previous one's weights in the
         Infinity Cache (the lm-head, 826 MB, cannot stay there either)."""
@@ -594,6 +594,17 @@ class Bench:
             ctx.gate_up_geglu_decode(g[i % 2], u[i % 2], N.CDNA4, D, F, xd, hdo)
         for i in range(n):  # config 2's block: gate/up + GeGLU and the Q6_K down in one launch
             ctx.ffn_block_decode(g[i % 2], u[i % 2], d6[i % 2], Q6, N.CDNA4, D, F, xd, hdo, yd2)
+        # config 4's decode layers in one launch: 8 layers over four distinct weight copies (460 MB,
+        # more than the Infinity Cache holds), Q6_K down on even layers and Q4_K on odd ones
+        g2, u2 = g + [self.weights(Q4, 0x9A + i, F, D) for i in range(2)], u + [self.weights(Q4, 0x9C + i, F, D) for i in range(2)]
+        d62, d42 = d6 + [self.weights(Q6, 0x9E + i, D, F) for i in range(2)], d4 + [self.weights(Q4, 0xA0 + i, D, F) for i in range(2)]
+        nw = [torch.ones(D, dtype=torch.float32, device="cuda") for _ in range(8)]
+        torch.cuda.synchronize()
+        for i in range(n):
+            ctx.ffn_stack_decode([g2[l % 4] for l in range(8)], [u2[l % 4] for l in range(8)],
+                                 [d62[l % 4] if l % 2 == 0 else d42[l % 4] for l in range(8)],
+                                 [Q6 if l % 2 == 0 else Q4 for l in range(8)], N.CDNA4, D, F, xd, hdo, yd2,
+                                 norm_weights=nw, eps=EPS)
         # batch 4 (MTP verification) on the matrix cores: the lm-head, the gate/up pair, the Q6_K down
         lm = self.weights(Q6, 0x1B, V, D)
         x4, xh4, hh4 = self.f32(0xB4, 4 * D), self.f16(0xB6, 4 * D), self.f16(0xB8, 4 * F)
